@@ -1,0 +1,85 @@
+// Device helpers shared by the gfx950 kernels: bfloat16 storage and rounding, wave64
+// reductions, MFMA operand types, and the PyTorch-compatible activations.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qwen3_5_ops.h"
+
+namespace q35 {
+
+// bfloat16 values are carried as raw 16-bit patterns in memory.
+using bf16 = uint16_t;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float f32(bf16 x) { return __uint_as_float((uint32_t)x << 16); }
+
+// Round to nearest even through the hardware conversion (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16 to_bf16(float x) {
+    __bf16 b = (__bf16)x;
+    return __builtin_bit_cast(uint16_t, b);
+}
+__device__ __forceinline__ float round_bf16(float x) { return f32(to_bf16(x)); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return (uint32_t)to_bf16(lo) | ((uint32_t)to_bf16(hi) << 16);
+}
+__device__ __forceinline__ float lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+// PyTorch's float32 SiLU and sigmoid: x / (1 + e^-x) and 1 / (1 + e^-x) with expf.
+__device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+
+// Butterfly sum over `width` consecutive lanes of a wave64 (width a power of two <= 64).
+template <int width>
+__device__ __forceinline__ float lane_sum(float x) {
+#pragma unroll
+    for (int o = width / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+template <int width>
+__device__ __forceinline__ float lane_max(float x) {
+#pragma unroll
+    for (int o = width / 2; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+// 8 bf16 as one 16-byte access.
+struct alignas(16) Pack8 {
+    uint32_t w[4];
+};
+
+__device__ __forceinline__ void unpack8(const Pack8& p, float out[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        out[2 * i] = lo_f32(p.w[i]);
+        out[2 * i + 1] = hi_f32(p.w[i]);
+    }
+}
+
+__device__ __forceinline__ Pack8 pack8(const float in[8]) {
+    Pack8 p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) p.w[i] = pack2(in[2 * i], in[2 * i + 1]);
+    return p;
+}
+
+// MFMA 16x16x32 bf16 -> f32 (gfx950). Operand layout for a wave:
+//   A (16 x 32): lane l holds row l % 16, k = 8 * (l / 16) + 0..7
+//   B (32 x 16): lane l holds col l % 16, k = 8 * (l / 16) + 0..7
+//   D (16 x 16): lane l holds col l % 16, rows 4 * (l / 16) + 0..3
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+inline unsigned cdiv(size_t n, unsigned d) { return (unsigned)((n + d - 1) / d); }
+
+}  // namespace q35

@@ -1,0 +1,232 @@
+"""Loader of libqwen3_5_hip.so, mirroring src/models/qwen3_5/native/src/cuda.rs.
+
+* ``load(path)`` resolves every symbol of the reference's ``api!`` table
+  (cuda.rs:50-133) plus this build's additions and fails if one is missing or if
+  ``cs1_abi_version() != 6`` (cuda.rs:146-168).
+* ``check(code, what)`` raises ``HipError`` for a non-zero return; codes >= 1000 are
+  hipBLASLt statuses (cuda.rs:177-187).
+* ``DeviceBuffer`` / ``Stream`` / ``Graph`` mirror cuda.rs:194-353.
+
+There is no fallback: if the library is missing or lacks a symbol, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_float, c_int, c_size_t, c_uint32, c_void_p
+
+import numpy as np
+
+ABI_VERSION = 6
+LIBRARY = "libqwen3_5_hip.so"
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+P = c_void_p
+_I = c_int
+_SZ = c_size_t
+
+# name -> (restype, argtypes): the reference table (cuda.rs:50-133) ...
+SYMBOLS = {
+    "cs1_vision_linear": (_I, [P, P, P, P, P, _I, _I, _I, P]),
+    "cs1_gemm_f32": (_I, [P, P, P, P, _I, _I, _I, P]),
+    "cs1_vision_norm": (_I, [P, P, P, P, _I, _I, P]),
+    "cs1_vision_position": (_I, [P, P, P, P, _I, P]),
+    "cs1_vision_rope": (_I, [P, P, P, P, P, _I, P]),
+    "cs1_vision_attention": (_I, [P, P, P, P, _I, P]),
+    "cs1_vision_bias": (_I, [P, P, _SZ, _I, P]),
+    "cs1_vision_gelu": (_I, [P, _SZ, _I, P]),
+    "cs1_vision_add": (_I, [P, P, _SZ, P]),
+    "cs1_vision_to_float": (_I, [P, P, _SZ, P]),
+    "cs1_vision_lora_add": (_I, [P, P, _SZ, c_float, P]),
+    "cs1_abi_version": (c_uint32, []),
+    "cs1_error_string": (ctypes.c_char_p, [_I]),
+    "cs1_set_device": (_I, [_I]),
+    "cs1_malloc": (_I, [ctypes.POINTER(c_void_p), _SZ]),
+    "cs1_free": (_I, [P]),
+    "cs1_stream_create": (_I, [ctypes.POINTER(c_void_p)]),
+    "cs1_stream_sync": (_I, [P]),
+    "cs1_stream_destroy": (_I, [P]),
+    "cs1_graph_begin": (_I, [P]),
+    "cs1_graph_end": (_I, [P, ctypes.POINTER(c_void_p)]),
+    "cs1_graph_launch": (_I, [P, P]),
+    "cs1_graph_destroy": (_I, [P]),
+    "cs1_upload": (_I, [P, P, _SZ, P]),
+    "cs1_download": (_I, [P, P, _SZ, P]),
+    "cs1_copy_dd": (_I, [P, P, _SZ, P]),
+    "cs1_copy2d": (_I, [P, _SZ, P, _SZ, _SZ, _SZ, P]),
+    "cs1_embed": (_I, [P, P, P, _I, _I, P]),
+    "cs1_rms_norm": (_I, [P, P, P, _I, _I, c_float, P]),
+    "cs1_add_rms_norm": (_I, [P, P, P, P, _I, _I, c_float, P]),
+    "cs1_gated_rms_norm": (_I, [P, P, _I, P, P, _I, _I, _I, c_float, P]),
+    "cs1_gdn_conv": (_I, [P, _I, P, P, P, P, _I, _I, _I, P]),
+    "cs1_gdn_gates": (_I, [P, P, _I, P, P, P, P, _I, _I, P]),
+    "cs1_gdn_workspace_floats": (_SZ, [_I, _I]),
+    "cs1_gdn_prefill": (_I, [P, P, P, P, P, P, P, _I, _I, _I, c_float, P]),
+    "cs1_gdn_prefill_x": (_I, [P, P, P, P, P, P, P, _I, _I, _I, c_float, P, P, P]),
+    "cs1_attn_prep": (_I, [P, P, _I, P, P, P, P, P, P, P, _I, _I, _I, _I, _I, c_float, P]),
+    "cs1_attention": (_I, [P, P, P, _I, P, _I, _I, _I, _I, c_float, P]),
+    "cs1_attention_gated": (_I, [P, P, P, _I, P, P, _I, _I, _I, _I, c_float, P]),
+    "cs1_attention_gated_prefix": (_I, [P, P, P, _I, P, P, _I, _I, _I, _I, c_float, _I, P]),
+    "cs1_sigmoid_gate": (_I, [P, P, _SZ, P]),
+    "cs1_silu_mul": (_I, [P, _I, P, _I, _I, P]),
+    "cs1_gemm_create": (P, [_SZ]),
+    "cs1_gemm_destroy": (None, [P]),
+    "cs1_gemm": (_I, [P, P, P, P, _I, _I, _I, _I, P]),
+}
+# ... and this build's additions (no reference counterpart)
+ADDITIONS = {
+    "cs1_attention_ex": (_I, [P, P, P, _I, P, P, P, _I, _I, _I, _I, c_float, _I, P]),
+}
+
+HIP_ERROR_INVALID_VALUE = 1
+HIP_ERROR_NOT_SUPPORTED = 801
+
+
+class HipError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+class Api:
+    """The resolved function table."""
+
+    def __init__(self, lib: ctypes.CDLL, path: str):
+        self._lib = lib
+        self.path = path
+        for name, (res, args) in {**SYMBOLS, **ADDITIONS}.items():
+            try:
+                fn = getattr(lib, name)
+            except AttributeError as e:
+                raise RuntimeError(f"{LIBRARY} has no {name}") from e
+            fn.restype = res
+            fn.argtypes = args
+            setattr(self, name, fn)
+
+
+_API: Api | None = None
+
+
+def default_library() -> str:
+    return os.environ.get("CS1_HIP_LIB", os.path.join(_PKG_ROOT, LIBRARY))
+
+
+def load(path: str | None = None) -> Api:
+    """Load the library once per process and check its ABI version (cuda.rs:146-168)."""
+    global _API
+    if _API is not None:
+        return _API
+    path = path or default_library()
+    if not os.path.exists(path):
+        raise RuntimeError(f"loading {path}: not built (run __graft_entry__.build())")
+    api = Api(ctypes.CDLL(path), path)
+    abi = api.cs1_abi_version()
+    if abi != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {abi}, this build needs {ABI_VERSION}; rebuild it")
+    _API = api
+    return api
+
+
+def api() -> Api:
+    if _API is None:
+        raise RuntimeError("the HIP library is not loaded")
+    return _API
+
+
+def check(code: int, what: str) -> None:
+    if code == 0:
+        return
+    if code >= 1000:
+        raise HipError(code, f"{what}: hipBLASLt status {code - 1000}")
+    msg = api().cs1_error_string(code)
+    raise HipError(code, f"{what}: {msg.decode() if msg else '?'} ({code})")
+
+
+def set_device(device: int = 0) -> None:
+    check(api().cs1_set_device(device), "hipSetDevice")
+
+
+class Stream:
+    def __init__(self):
+        h = c_void_p()
+        check(api().cs1_stream_create(ctypes.byref(h)), "hipStreamCreateWithFlags")
+        self.handle = h.value
+
+    def sync(self):
+        check(api().cs1_stream_sync(self.handle), "hipStreamSynchronize")
+
+    def destroy(self):
+        if self.handle:
+            api().cs1_stream_destroy(self.handle)
+            self.handle = None
+
+
+class DeviceBuffer:
+    """A device allocation freed on drop (cuda.rs:194-228)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        self.ptr = None
+        if self.nbytes > 0:
+            p = c_void_p()
+            check(api().cs1_malloc(ctypes.byref(p), self.nbytes), "hipMalloc")
+            self.ptr = p.value
+
+    def at(self, offset: int = 0):
+        assert 0 <= offset <= self.nbytes
+        return None if self.ptr is None else self.ptr + offset
+
+    def __del__(self):
+        if getattr(self, "ptr", None) and _API is not None:
+            _API.cs1_free(self.ptr)
+            self.ptr = None
+
+
+def to_device(arr: np.ndarray, stream: Stream) -> DeviceBuffer:
+    arr = np.ascontiguousarray(arr)
+    buf = DeviceBuffer(arr.nbytes)
+    if arr.nbytes:
+        check(api().cs1_upload(buf.at(0), arr.ctypes.data, arr.nbytes, stream.handle), "copy to device")
+    return buf
+
+
+def upload(buf: DeviceBuffer, arr: np.ndarray, stream: Stream, offset: int = 0) -> None:
+    arr = np.ascontiguousarray(arr)
+    check(api().cs1_upload(buf.at(offset), arr.ctypes.data, arr.nbytes, stream.handle), "copy to device")
+
+
+def from_device(buf: DeviceBuffer, dtype, count: int, stream: Stream, offset: int = 0) -> np.ndarray:
+    out = np.empty(count, dtype=dtype)
+    if out.nbytes:
+        check(api().cs1_download(out.ctypes.data, buf.at(offset), out.nbytes, stream.handle), "copy to host")
+    return out
+
+
+class Graph:
+    """Capture what ``record`` queues on ``stream`` and instantiate it (cuda.rs:307-353)."""
+
+    def __init__(self, stream: Stream, record):
+        check(api().cs1_graph_begin(stream.handle), "hipStreamBeginCapture")
+        err = None
+        try:
+            record()
+        except Exception as e:  # the capture is always ended
+            err = e
+        exec_ = c_void_p()
+        code = api().cs1_graph_end(stream.handle, ctypes.byref(exec_))
+        self.exec = exec_.value
+        if err is not None or code != 0:
+            if self.exec:
+                api().cs1_graph_destroy(self.exec)
+                self.exec = None
+            if err is not None:
+                raise err
+            check(code, "capturing a HIP graph")
+
+    def launch(self, stream: Stream):
+        check(api().cs1_graph_launch(self.exec, stream.handle), "hipGraphLaunch")
+
+    def __del__(self):
+        if getattr(self, "exec", None) and _API is not None:
+            _API.cs1_graph_destroy(self.exec)
+            self.exec = None

@@ -1,0 +1,214 @@
+"""GPU parity of the HBM-bound prefill kernels: conv1d + SiLU, gates, gated RMSNorm,
+attn_prep (RMSNorm + RoPE), residual norms, SwiGLU, sigmoid gate, embedding, copies.
+
+Mirrors tests/qwen3_5/kernels.rs:65-199, 744-850. The bar is the reference's: at most
+one bf16 ulp from the emulated reference kernel (float32 expf/rsqrt may differ by an
+ulp between devices), bit-for-bit for pure data movement and for the packed vs scalar
+paths.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import dev, empty, get, get_bf16, say, stream, ulp_diff
+from qwen3_5_native import hip
+
+pytestmark = pytest.mark.gpu
+
+
+def rnd(n, seed, amp=1.0):
+    return O.xorshift_bf16(n, seed, amp)
+
+
+@pytest.mark.parametrize("T,key_dim,value_dim,pad", [(8192, 2048, 4096, 0), (130, 256, 512, 192), (37, 16, 24, 8),
+                                                     (5, 12, 20, 3)])
+def test_gdn_conv_matches_emulator(T, key_dim, value_dim, pad):
+    api, st = hip.api(), stream()
+    ch = 2 * key_dim + value_dim
+    ld = ch + pad
+    say(f"gdn_conv T={T} key_dim={key_dim} value_dim={value_dim} ld={ld}")
+    x = rnd(T * ld, 21, 2.0)
+    w = O.f32_to_bf16((np.random.default_rng(0).standard_normal(ch * 4) * 0.5).astype(np.float32))
+    dx, dw = dev(x), dev(w)
+    q, k, v = empty(T * key_dim * 2), empty(T * key_dim * 2), empty(T * value_dim * 2)
+    hip.check(api.cs1_gdn_conv(dx.at(0), ld, dw.at(0), q.at(0), k.at(0), v.at(0), T, key_dim, value_dim, st.handle),
+              "conv")
+    eq, ek, ev = O.gdn_conv(x, ld, w, T, key_dim, value_dim)
+    for name, got, want in (("q", get_bf16(q, T * key_dim), eq), ("k", get_bf16(k, T * key_dim), ek),
+                            ("v", get_bf16(v, T * value_dim), ev)):
+        d = ulp_diff(got, want)
+        say(f"  {name}: max ulp {d}, exact {np.mean(got == want):.4f}")
+        assert d <= 1
+        assert np.mean(got == want) > 0.99
+
+
+def test_gdn_conv_continuation_uses_cached_history():
+    # kernels.rs:771-850: restoring three cached rows reproduces the full pass bit for bit
+    api, st = hip.api(), stream()
+    prefix = 64
+    key_dim, value_dim, heads = 16 * 128, 48 * 128, 48
+    ch = 2 * key_dim + value_dim
+    ld = ch + value_dim + 2 * heads
+    w = dev(np.full(ch * 4, O.f32_to_bf16(np.float32([0.25]))[0], np.uint16))
+
+    def conv(src, start, rows):
+        q, k, v = empty(rows * key_dim * 2), empty(rows * key_dim * 2), empty(rows * value_dim * 2)
+        hip.check(api.cs1_gdn_conv(src.at(start * ld * 2), ld, w.at(0), q.at(0), k.at(0), v.at(0), rows, key_dim,
+                                   value_dim, st.handle), "conv continuation")
+        return [get_bf16(q, rows * key_dim), get_bf16(k, rows * key_dim), get_bf16(v, rows * value_dim)]
+
+    for rows in [1, 2, 3, 4, 65]:
+        say(f"conv continuation rows={rows}")
+        total = prefix + rows
+        proj = O.f32_to_bf16(np.abs(O.bf16_to_f32(rnd(total * ld, 37, 0.5))) + np.float32(0.25))
+        src = dev(proj)
+        full = conv(src, 0, total)
+        tail, window = empty(3 * ld * 2), empty((rows + 3) * ld * 2)
+        hip.check(api.cs1_copy_dd(tail.at(0), src.at((prefix - 3) * ld * 2), 3 * ld * 2, st.handle), "copy")
+        hip.check(api.cs1_copy_dd(window.at(0), tail.at(0), 3 * ld * 2, st.handle), "copy")
+        hip.check(api.cs1_copy_dd(window.at(3 * ld * 2), src.at(prefix * ld * 2), rows * ld * 2, st.handle), "copy")
+        restored = conv(window, 0, rows + 3)
+        missing = conv(window, 3, rows)
+        for i, width in enumerate([key_dim, key_dim, value_dim]):
+            want = full[i][prefix * width:]
+            np.testing.assert_array_equal(restored[i][3 * width:], want)
+            m = min(rows, 3) * width
+            assert not np.array_equal(missing[i][:m], want[:m])
+
+
+def test_gdn_gates_match_emulator():
+    api, st = hip.api(), stream()
+    T, H, ld = 4096, 32, 2 * 32 + 40
+    say("gdn_gates")
+    rng = np.random.default_rng(3)
+    b = O.f32_to_bf16((rng.standard_normal(T * ld) * 3).astype(np.float32))
+    a = O.f32_to_bf16((rng.standard_normal(T * ld) * 8).astype(np.float32))
+    A_log = O.f32_to_bf16(np.log(rng.uniform(0.01, 16, H)).astype(np.float32))
+    dt = O.f32_to_bf16(np.ones(H, np.float32))
+    db, da, dA, ddt = dev(b), dev(a), dev(A_log), dev(dt)
+    beta, g = empty(T * H * 2), empty(T * H * 4)
+    hip.check(api.cs1_gdn_gates(db.at(0), da.at(0), ld, dA.at(0), ddt.at(0), beta.at(0), g.at(0), T, H, st.handle),
+              "gates")
+    eb, eg = O.gdn_gates(b, a, ld, A_log, dt, T, H)
+    assert ulp_diff(get_bf16(beta, T * H), eb) <= 1
+    np.testing.assert_allclose(get(g, np.float32, T * H), eg, rtol=2e-6, atol=1e-30)
+
+
+@pytest.mark.parametrize("T,H,extra", [(8192, 32, 0), (77, 6, 40)])
+def test_gated_rms_norm_matches_emulator(T, H, extra):
+    api, st = hip.api(), stream()
+    D = 128
+    ldz = H * D + extra
+    say(f"gated_rms_norm T={T} H={H} ldz={ldz}")
+    x = rnd(T * H * D, 41, 3.0)
+    z = rnd(T * ldz, 42, 4.0)
+    w = O.f32_to_bf16(np.random.default_rng(1).uniform(0.5, 1.5, D).astype(np.float32))
+    out = empty(T * H * D * 2)
+    dx, dz, dw = dev(x), dev(z), dev(w)
+    hip.check(api.cs1_gated_rms_norm(dx.at(0), dz.at(0), ldz, dw.at(0), out.at(0), T, H, D, 1e-6, st.handle), "norm")
+    got = get_bf16(out, T * H * D)
+    want = O.gated_rms_norm(x, z, ldz, w, T, H, D, 1e-6)
+    assert ulp_diff(got, want) <= 1
+    assert np.mean(got == want) > 0.99
+
+
+@pytest.mark.parametrize("Dh,Hq,Hk,half", [(256, 16, 4, 32), (128, 16, 4, 32), (256, 24, 4, 64), (128, 8, 2, 16)])
+def test_attn_prep_matches_emulator(Dh, Hq, Hk, half):
+    api, st = hip.api(), stream()
+    T = 333
+    ld = Hq * 2 * Dh + 2 * Hk * Dh + 16
+    say(f"attn_prep Dh={Dh} Hq={Hq} Hk={Hk} half={half}")
+    row = rnd(T * ld, 51, 2.0)
+    kr_off = Hq * 2 * Dh
+    qw = O.f32_to_bf16((np.random.default_rng(2).standard_normal(Dh) * 0.1).astype(np.float32))
+    kw = O.f32_to_bf16((np.random.default_rng(3).standard_normal(Dh) * 0.1).astype(np.float32))
+    cs, sn = O.rotary_tables(np.arange(T, dtype=np.int64) * 3, half, 1e7)
+    drow, dqw, dkw, dcs, dsn = dev(row), dev(qw), dev(kw), dev(cs), dev(sn)
+    q, gate, k = empty(T * Hq * Dh * 2), empty(T * Hq * Dh * 2), empty(T * Hk * Dh * 2)
+    hip.check(api.cs1_attn_prep(drow.at(0), drow.at(kr_off * 2), ld, dqw.at(0), dkw.at(0), dcs.at(0), dsn.at(0),
+                                q.at(0), gate.at(0), k.at(0), T, Hq, Hk, Dh, half, 1e-6, st.handle), "attn_prep")
+    kr = np.concatenate([row[kr_off:], np.zeros(kr_off, np.uint16)])
+    eq, eg, ek = O.attn_prep(row, kr, ld, qw, kw, cs, sn, T, Hq, Hk, Dh, half, 1e-6)
+    np.testing.assert_array_equal(get_bf16(gate, T * Hq * Dh), eg)
+    for got, want in ((get_bf16(q, T * Hq * Dh), eq), (get_bf16(k, T * Hk * Dh), ek)):
+        # one ulp in the norm can move the rotated sum by one more rounding step
+        assert ulp_diff(got, want) <= 2
+        assert np.mean(got == want) > 0.99
+
+
+@pytest.mark.parametrize("D,offset", [(2560, 0), (5120, 0), (8192, 0), (257, 0), (8448, 0), (2560, 8)])
+def test_residual_rms_norm_matches_rounded_reference(D, offset):
+    # kernels.rs:65-144: the residual add is exact, the norm within one bf16 ulp
+    api, st = hip.api(), stream()
+    rows = 37
+    say(f"rms norms D={D} offset={offset}")
+    x = rnd(rows * D + offset, 61, 3.0)
+    dl = rnd(rows * D + offset, 62, 1.0)
+    w = rnd(D, 63, 0.2)
+    dx, dd, dw = dev(x), dev(dl), dev(w)
+    out = empty((rows * D + offset) * 2)
+    hip.check(api.cs1_rms_norm(dx.at(offset * 2), dw.at(0), out.at(offset * 2), rows, D, 1e-6, st.handle), "rms")
+    want = O.rms_norm(x[offset:], w, rows, D)
+    assert ulp_diff(get_bf16(out, rows * D, offset * 2), want) <= 1
+    hip.check(api.cs1_add_rms_norm(dx.at(offset * 2), dd.at(offset * 2), dw.at(0), out.at(offset * 2), rows, D, 1e-6,
+                                   st.handle), "add rms")
+    res, want = O.add_rms_norm(x[offset:], dl[offset:], w, rows, D)
+    np.testing.assert_array_equal(get_bf16(dx, rows * D, offset * 2), res)
+    assert ulp_diff(get_bf16(out, rows * D, offset * 2), want) <= 1
+
+
+def test_silu_mul_packed_equals_scalar_and_reference():
+    api, st = hip.api(), stream()
+    T, I = 300, 9728
+    say("silu_mul")
+    gu = rnd(T * 2 * I + 1, 71, 6.0)
+    dg = dev(gu)
+    a, b = empty(T * I * 2), empty(T * I * 2 + 2)
+    hip.check(api.cs1_silu_mul(dg.at(0), 2 * I, a.at(0), T, I, st.handle), "packed")
+    hip.check(api.cs1_silu_mul(dg.at(2), 2 * I, b.at(2), T, I, st.handle), "scalar (misaligned)")
+    packed = get_bf16(a, T * I)
+    scalar_in = gu[1:]
+    assert ulp_diff(get_bf16(b, T * I, 2), O.silu_mul(np.ascontiguousarray(scalar_in), 2 * I, T, I)) <= 1
+    assert ulp_diff(packed, O.silu_mul(gu[:-1], 2 * I, T, I)) <= 1
+    # same inputs through both paths: bit-identical
+    c = empty(T * I * 2 + 2)
+    dg2 = empty(T * 2 * I * 2 + 2)
+    hip.check(api.cs1_copy_dd(dg2.at(2), dg.at(0), T * 2 * I * 2, st.handle), "copy")
+    hip.check(api.cs1_silu_mul(dg2.at(2), 2 * I, c.at(2), T, I, st.handle), "scalar")
+    np.testing.assert_array_equal(get_bf16(c, T * I, 2), packed)
+
+
+def test_sigmoid_gate_vector_and_scalar():
+    api, st = hip.api(), stream()
+    n = 4096 * 16
+    say("sigmoid gate")
+    x, g = rnd(n + 1, 81, 2.0), rnd(n + 1, 82, 12.0)
+    g[:3] = O.f32_to_bf16(np.float32([-40.0, 40.0, 0.0]))
+    want = O.sigmoid_gate(x[:n], g[:n])
+    dx, dg = dev(x), dev(g)
+    hip.check(api.cs1_sigmoid_gate(dx.at(0), dg.at(0), n, st.handle), "vector gate")
+    assert ulp_diff(get_bf16(dx, n), want) <= 1
+    dx2 = dev(x)
+    hip.check(api.cs1_sigmoid_gate(dx2.at(2), dg.at(2), n, st.handle), "scalar gate")
+    assert ulp_diff(get_bf16(dx2, n, 2), O.sigmoid_gate(x[1:], g[1:])) <= 1
+
+
+def test_embed_and_device_copies():
+    api, st = hip.api(), stream()
+    V, D, T = 1000, 2560, 257
+    say("embed and copies")
+    table = rnd(V * D, 91, 1.0)
+    ids = np.random.default_rng(4).integers(0, V, T).astype(np.int32)
+    dt, di, out = dev(table), dev(ids), empty(T * D * 2)
+    hip.check(api.cs1_embed(di.at(0), dt.at(0), out.at(0), T, D, st.handle), "embed")
+    np.testing.assert_array_equal(get_bf16(out, T * D).reshape(T, D), table.reshape(V, D)[ids])
+    # kernels.rs:744-769
+    a = dev(rnd(4099, 1, 2.0))
+    b = empty(4099 * 2)
+    hip.check(api.cs1_copy_dd(b.at(0), a.at(0), 4099 * 2, st.handle), "copy_dd")
+    np.testing.assert_array_equal(get_bf16(a, 4099), get_bf16(b, 4099))
+    rows, ld, w = 5, 300, 256
+    srcv = rnd(rows * ld, 2, 1.0)
+    src, dst = dev(srcv), empty(rows * w * 2)
+    hip.check(api.cs1_copy2d(dst.at(0), w * 2, src.at(0), ld * 2, w * 2, rows, st.handle), "copy2d")
+    np.testing.assert_array_equal(get_bf16(dst, rows * w).reshape(rows, w), srcv.reshape(rows, ld)[:, :w])
