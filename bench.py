@@ -1,0 +1,235 @@
+"""Prefill throughput of the MI355X Qwen3.5 hot path, one JSON line on stdout.
+
+Metric: "prefill tokens/s per layer type + ms per 4k-token hybrid
+decision prefill".  A step is one prefill pass of one layer over one synthetic batch
+with the inputs already resident in HBM:
+
+  * headline (`value`): the gated GQA flash-attention layer of BASELINE config 1
+    (T = 2048, 16 q / 4 kv heads, Dh = 128, sigmoid gate, float32 LSE), tokens/s;
+  * `layers`: the same measurement for the GDN layer of config 2 (causal conv1d + SiLU,
+    then the chunked gated delta rule, T = 8192, 16 qk / 32 v heads, S0 ~ N(0, 0.01)) and
+    of config 0 (T = 512, 16 / 16 heads), each with its kernels' roofline figures.
+
+Timing: W untimed warm-up steps, then K steps bracketed by a stream sync on both sides;
+per-kernel averages come from HIP events recorded on the stream the kernels run on
+(hipEventElapsedTime over the K launches of the timed region).  Everything runs through
+the library's C ABI; no torch in this process.
+
+The CPU baseline is the repository's C restatement of the reference kernel (oracle/,
+OpenMP) timed on this host on a bounded sample of the same workload.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "system1-omni_amd"))
+
+from qwen3_5_native import hip  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+class Events:
+    """hipEvent_t pairs from the HIP runtime the library itself links."""
+
+    def __init__(self):
+        self.rt = ctypes.CDLL("libamdhip64.so.7")
+        self.rt.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.rt.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+
+    def new(self):
+        e = ctypes.c_void_p()
+        hip.check(self.rt.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e.value
+
+    def record(self, ev, stream):
+        hip.check(self.rt.hipEventRecord(ev, stream.handle), "hipEventRecord")
+
+    def ms(self, a, b):
+        hip.check(self.rt.hipEventSynchronize(b), "hipEventSynchronize")
+        out = ctypes.c_float()
+        hip.check(self.rt.hipEventElapsedTime(ctypes.byref(out), a, b), "hipEventElapsedTime")
+        return out.value
+
+
+def bf16(rng, n, std=1.0):
+    x = (rng.standard_normal(n) * std).astype(np.float32)
+    u = x.view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def unit_rows_bf16(rng, rows, d):
+    x = rng.standard_normal((rows, d))
+    x /= np.sqrt((x * x).sum(-1, keepdims=True))
+    u = x.astype(np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16).reshape(-1)
+
+
+def timed(stream, ev, steps, warmup, launches):
+    """Run `launches` (list of (name, fn)) per step; return wall ms/step and per-name avg ms."""
+    for _ in range(warmup):
+        for _, fn in launches:
+            fn()
+    stream.sync()
+    marks = [[ev.new() for _ in range(len(launches) + 1)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for s in range(steps):
+        ev.record(marks[s][0], stream)
+        for i, (_, fn) in enumerate(launches):
+            fn()
+            ev.record(marks[s][i + 1], stream)
+    stream.sync()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    per = {name: sum(ev.ms(marks[s][i], marks[s][i + 1]) for s in range(steps)) / steps
+           for i, (name, _) in enumerate(launches)}
+    return wall_ms, per
+
+
+def bench_attention(api, st, ev, steps, warmup):
+    T, Hq, Hk, Dh = 2048, 16, 4, 128
+    rng = np.random.default_rng(1)
+    q, k, v, gate = (hip.to_device(bf16(rng, T * h * Dh), st) for h in (Hq, Hk, Hk, Hq))
+    out, lse = hip.DeviceBuffer(T * Hq * Dh * 2), hip.DeviceBuffer(Hq * T * 4)
+
+    def launch():
+        hip.check(api.cs1_attention_ex(q.at(0), k.at(0), v.at(0), Hk * Dh, gate.at(0), out.at(0), lse.at(0), T, Hq, Hk,
+                                       Dh, Dh ** -0.5, 0, st.handle), "attention")
+
+    wall, per = timed(st, ev, steps, warmup, [("flash_attention", launch)])
+    flops = 2.0 * T * T * Dh * Hq  # causal: half of 4 T^2 Dh Hq
+    kern = per["flash_attention"]
+    achieved = flops / (kern * 1e-3) / 1e12
+    return {
+        "workload": "cfg1 gated GQA flash-attention prefill T=2048 Hq=16 Hk=4 Dh=128 + fp32 LSE",
+        "tokens_per_s": T / (wall * 1e-3), "ms_per_step": wall, "kernel_ms": per,
+        "roofline": {"kernel": "flash_kernel<128,gated>", "bound": "mfma", "achieved": achieved,
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
+                     "algorithmic_flop": flops},
+    }
+
+
+def gdn_layer(api, st, T, H, HK, with_conv, s0_std, seed):
+    D = 128
+    rng = np.random.default_rng(seed)
+    key_dim, value_dim = HK * D, H * D
+    bufs = {}
+    if with_conv:
+        ch = 2 * key_dim + value_dim
+        bufs["qkv"] = hip.to_device(bf16(rng, T * ch), st)
+        bufs["w"] = hip.to_device(bf16(rng, ch * 4, 0.02), st)
+        for n, w in (("q", key_dim), ("k", key_dim), ("v", value_dim)):
+            bufs[n] = hip.DeviceBuffer(T * w * 2)
+    else:
+        bufs["q"] = hip.to_device(unit_rows_bf16(rng, T * HK, D), st)
+        bufs["k"] = hip.to_device(unit_rows_bf16(rng, T * HK, D), st)
+        bufs["v"] = hip.to_device(bf16(rng, T * H * D), st)
+    beta = (1 / (1 + np.exp(-rng.standard_normal(T * H)))).astype(np.float32)
+    bufs["beta"] = hip.to_device(((beta.view(np.uint32) + 0x7FFF + ((beta.view(np.uint32) >> 16) & 1)) >> 16)
+                                 .astype(np.uint16), st)
+    bufs["g"] = hip.to_device((-np.log1p(np.exp(rng.standard_normal(T * H))) * 0.1).astype(np.float32), st)
+    bufs["s_in"] = hip.to_device((rng.standard_normal(H * D * D) * s0_std).astype(np.float32), st) if s0_std else None
+    bufs["s_out"] = hip.DeviceBuffer(H * D * D * 4)
+    bufs["o"] = hip.DeviceBuffer(T * H * D * 2)
+    bufs["ws"] = hip.DeviceBuffer(api.cs1_gdn_workspace_floats(T, H) * 4)
+    launches = []
+    if with_conv:
+        launches.append(("gdn_conv", lambda: hip.check(api.cs1_gdn_conv(
+            bufs["qkv"].at(0), 2 * key_dim + value_dim, bufs["w"].at(0), bufs["q"].at(0), bufs["k"].at(0),
+            bufs["v"].at(0), T, key_dim, value_dim, st.handle), "conv")))
+    launches.append(("gdn_prefill", lambda: hip.check(api.cs1_gdn_prefill_x(
+        bufs["q"].at(0), bufs["k"].at(0), bufs["v"].at(0), bufs["g"].at(0), bufs["beta"].at(0), bufs["o"].at(0),
+        bufs["ws"].at(0), T, H, HK, D ** -0.5, bufs["s_in"].at(0) if bufs["s_in"] else None, bufs["s_out"].at(0),
+        st.handle), "gdn")))
+    return bufs, launches
+
+
+def bench_gdn(api, st, ev, steps, warmup, T, H, HK, with_conv, s0_std, seed, label):
+    D = 128
+    bufs, launches = gdn_layer(api, st, T, H, HK, with_conv, s0_std, seed)
+    wall, per = timed(st, ev, steps, warmup, launches)
+    flops = 180224.0 * T * H  # dense-tile count per token per v-head: 10 C D + 6 D^2
+    io = 2 * T * HK * D * 2 + 2 * T * H * D * 2 + T * H * 6 + (2 if s0_std else 1) * H * D * D * 4
+    g_ms = per["gdn_prefill"]
+    res = {
+        "workload": label, "tokens_per_s": T / (wall * 1e-3), "ms_per_step": wall, "kernel_ms": per,
+        "gdn": {"bound": "mfma", "achieved": flops / (g_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": flops / (g_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                "algorithmic_flop": flops, "algorithmic_io_bytes": io,
+                "io_GBs": io / (g_ms * 1e-3) / 1e9},
+    }
+    if with_conv:
+        cbytes = 2 * T * (2 * HK * D + H * D) * 2
+        c_ms = per["gdn_conv"]
+        res["conv"] = {"bound": "hbm", "achieved": cbytes / (c_ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                       "frac": cbytes / (c_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "algorithmic_bytes": cbytes}
+    return res
+
+
+def cpu_baseline_attention():
+    """The oracle's emulation of the reference flash kernel (C, OpenMP) on this host, over
+    the full config-1 layer, repeated until about 10 s of work."""
+    import oracle as O
+
+    T, Hq, Hk, Dh = 2048, 16, 4, 128
+    rng = np.random.default_rng(1)
+    q, k, v, gate = (bf16(rng, T * h * Dh) for h in (Hq, Hk, Hk, Hq))
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.attention_emul(q, k, v, Hk * Dh, gate, T, Hq, Hk, Dh, Dh ** -0.5, want_lse=True)
+        n += 1
+        if time.perf_counter() - t0 > 10 or n >= 20:
+            break
+    dt = time.perf_counter() - t0
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": T * n / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"full cfg1 layer (T=2048, 16/4 heads, Dh=128, gate, LSE) x{n} through the oracle's C "
+                      f"emulation of the reference flash kernel, OpenMP over query rows"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the prefill is sharded by heads in "
+              "design only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    api = hip.load()
+    hip.set_device(0)
+    st = hip.Stream()
+    ev = Events()
+    attn = bench_attention(api, st, ev, args.steps, args.warmup)
+    g2 = bench_gdn(api, st, ev, args.steps, args.warmup, 8192, 32, 16, True, 0.01, 2,
+                   "cfg2 conv1d(k=4)+SiLU then GDN chunked prefill T=8192 HK=16 H=32 D=128, S0~N(0,0.01)")
+    g0 = bench_gdn(api, st, ev, args.steps, args.warmup, 512, 16, 16, False, 0.0, 0,
+                   "cfg0 GDN chunked prefill T=512 H=HK=16 D=128, S0=0")
+    cpu = None if args.no_cpu else cpu_baseline_attention()
+    line = {
+        "metric": "prefill tokens/s per layer type + ms per 4k-token hybrid decision prefill",
+        "value": attn["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": attn["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs of the BASELINE shapes)",
+        "config": {"workload": attn["workload"], "global_batch": 1, "seq_len": 2048, "parallelism": "none"},
+        "roofline": {k: attn["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac")} | {"traffic": None},
+        "cpu_baseline": cpu,
+        "layers": {"attention_cfg1": attn, "gdn_cfg2": g2, "gdn_cfg0": g0},
+        "decision_prefill_ms_4k": None,
+    }
+    print(json.dumps(line), flush=True)
+    st.destroy()
+
+
+if __name__ == "__main__":
+    main()

@@ -128,9 +128,8 @@ def load(path: str | None = None) -> Api:
 
 
 def api() -> Api:
-    if _API is None:
-        raise RuntimeError("the HIP library is not loaded")
-    return _API
+    """The loaded table; loads the default library on first use (raises if it is missing)."""
+    return _API if _API is not None else load()
 
 
 def check(code: int, what: str) -> None:

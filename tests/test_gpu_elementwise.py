@@ -108,8 +108,9 @@ def test_gated_rms_norm_matches_emulator(T, H, extra):
     hip.check(api.cs1_gated_rms_norm(dx.at(0), dz.at(0), ldz, dw.at(0), out.at(0), T, H, D, 1e-6, st.handle), "norm")
     got = get_bf16(out, T * H * D)
     want = O.gated_rms_norm(x, z, ldz, w, T, H, D, 1e-6)
-    assert ulp_diff(got, want) <= 1
-    assert np.mean(got == want) > 0.99
+    # two rounded products before the gate: an ulp of rsqrt can surface as two ulps
+    assert ulp_diff(got, want) <= 2
+    assert np.mean(got == want) > 0.999
 
 
 @pytest.mark.parametrize("Dh,Hq,Hk,half", [(256, 16, 4, 32), (128, 16, 4, 32), (256, 24, 4, 64), (128, 8, 2, 16)])
@@ -131,8 +132,11 @@ def test_attn_prep_matches_emulator(Dh, Hq, Hk, half):
     eq, eg, ek = O.attn_prep(row, kr, ld, qw, kw, cs, sn, T, Hq, Hk, Dh, half, 1e-6)
     np.testing.assert_array_equal(get_bf16(gate, T * Hq * Dh), eg)
     for got, want in ((get_bf16(q, T * Hq * Dh), eq), (get_bf16(k, T * Hk * Dh), ek)):
-        # one ulp in the norm can move the rotated sum by one more rounding step
-        assert ulp_diff(got, want) <= 2
+        # RoPE adds two rounded products that can cancel, so an ulp of the normalised
+        # input moves a tiny sum by many of its own ulps: bound the error by two ulps of
+        # the operands' magnitude (O(1) after the norm) instead
+        d = np.abs(O.bf16_to_f32(got) - O.bf16_to_f32(want))
+        assert (d <= 2 * 2.0 ** -8 * np.maximum(np.abs(O.bf16_to_f32(want)), 1.0)).all(), d.max()
         assert np.mean(got == want) > 0.99
 
 
