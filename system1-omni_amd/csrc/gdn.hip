@@ -6,24 +6,36 @@
 //     q^ = q rsqrt(|q|^2 + 1e-6) scale, k^ = k rsqrt(|k|^2 + 1e-6)  (float32);
 //     A_ij = (beta_i (k^_i . k^_j)) e^(cum_i - cum_j) for j < i, P_ij = (q^_i . k^_j) e^(...)
 //       for j <= i, the pair products on TF32-rounded operands with float32 sums;
-//     T = (I + A)^-1 by the blocked float32 substitution of gdn_prefill.cu:250-287;
-//     u = bf16(bf16(T beta) v), w = bf16(bf16(T beta) bf16(k^ e^cum)),
-//     qd = bf16(q^ e^cum), kd = bf16(k^ e^(cum_last - cum)), pb = bf16(P);
+//     T = (I + A)^-1 (float32, 16x16 blocks); tb = bf16(T_ij beta_j);
+//     u = bf16(tb v), w = bf16(tb bf16(k^ e^cum)), qd = bf16(q^ e^cum),
+//     kd = bf16(k^ e^(cum_last - cum)), pb = bf16(P);
 //   scan over chunks:  Sb = bf16(S); v_new = bf16(u - w Sb); o = bf16(qd Sb + pb v_new);
 //     S = S decay + kd^T v_new (float32).
 //
-// MI355X design (not the reference's three-kernel split):
-//   gdn_prep  grid (chunk, head), 8 waves.  TF32 operands are split exactly into two
-//     bf16 planes (hi = rne(x), lo = x - hi, exact since TF32 has 11 significant bits) so
-//     the TF32 pair products run on the bf16 MFMA (four products per term reproduce the
-//     TF32 product exactly); u and w are MFMA products of the triangular T with V and
-//     k e^cum staged transposed in LDS.
-//   gdn_scan  grid (head x 8 value slices of 16 columns), 4 waves.  The float32 state
-//     slice 128 x 16 lives in MFMA accumulators; each chunk reads w, qd, pb, kd^T rows
-//     straight from HBM/L2 into MFMA operand registers (prefetched one chunk ahead) and
-//     exchanges only bf16(S) and v_new through LDS.  The output o = qd Sb + pb v_new is
-//     produced in the same pass, so the per-chunk state copies and v_new never go to
-//     memory.  Slices of one head are issued to the same XCD (block = slice * H + head).
+// MI355X design.  Everything is organised around the operand layouts of the wave64 MFMA
+// v_mfma_f32_16x16x32_bf16 (lane l: A row / B column l % 16, k = 8 (l / 16) + e):
+//
+//   * One k ordering everywhere: within each 32-wide k step, lane group g holds
+//     k = {4g .. 4g+3, 16+4g .. 16+4g+3}.  With that ordering the accumulators of two
+//     16-row tiles (rows 4g + r of each) are, lane for lane, the B (or A) operand of the
+//     next MFMA, so products chain without moving data between lanes.
+//   * gdn_prep, grid (chunk, head), 4 waves, ~50 KB LDS (three blocks per CU):
+//       - TF32 pair products on the bf16 MFMA: each TF32 operand is split exactly into
+//         hi = rne_bf16(x) and lo = x - hi (TF32 has 11 significant bits), and the four
+//         products hi.hi + hi.lo + lo.hi + lo.lo reproduce the TF32 product exactly;
+//       - token-major inputs are transposed on the MFMA (a product with a 0/1 selection
+//         matrix, exact in bf16), not through LDS;
+//       - the triangular inverse: diagonal 16x16 blocks by forward substitution (the
+//         reference order), off-diagonal levels T_ij = -T_ii sum_k A_ik T_kj on the
+//         float32 MFMA v_mfma_f32_16x16x4_f32;
+//       - every scan operand is written to the workspace in the exact per-lane order the
+//         scan's MFMA consumes it (1 KB per wave per store, fully coalesced).
+//   * gdn_scan, grid (head x 8 slices of 16 value columns), 4 waves.  The float32 state
+//     slice 128 x 16 lives in MFMA accumulators; each chunk streams its operand
+//     fragments from HBM/L2 straight into registers (two chunks ahead) and exchanges only
+//     bf16(S) and v_new through LDS.  The output o = qd Sb + pb v_new is produced in the
+//     same pass, so per-chunk states and v_new never go to memory.  The slices of one head
+//     run on the same XCD (block = slice * H + head) and share its L2.
 #include "common.h"
 
 namespace q35 {
@@ -31,23 +43,31 @@ namespace {
 
 constexpr int C = 64;    // chunk length
 constexpr int DK = 128;  // key / value head dim
+constexpr uint32_t BF16_ONE = 0x3f80u;
 
 // ------------------------------------------------------------ workspace layout
 
-// Per (head, chunk) records, 256-byte aligned parts:
-//   w, u, qd  [64][128] bf16 row-major;  kdT [128][64] bf16 (kd transposed);
-//   pb [64][64] bf16 (zero above the diagonal);  decay float.
+// Per (head, chunk) record rec = head * NC + chunk; a "fragment" is 64 lanes x 8 bf16.
+//   w   [4 row blocks][4 dim steps]   fragments: lane = (row 16 it + l%16, dims 32 s + perm)
+//   qd  [4][4]                        same layout
+//   kd  [8 dim blocks][2 token steps] fragments: lane = (dim 16 b + l%16, tokens 32 s + perm)
+//   pb  [4 row blocks][2 token steps] fragments: lane = (row, tokens 32 s + perm), zero above
+//   u   [4 row blocks][8 dim blocks]  accumulator tiles: lane = (dim 16 dt + l%16,
+//                                     rows 16 it + 4 (l/16) + r), 4 bf16 per lane
+//   decay float
 struct Work {
-    bf16* w;
-    bf16* u;
-    bf16* qd;
-    bf16* kdt;
-    bf16* pb;
+    u32x4* w;
+    u32x4* qd;
+    u32x4* kd;
+    u32x4* pb;
+    u32x2* u;
     float* decay;
 };
 
+constexpr size_t FRAG = 64;  // lanes per fragment (u32x4 or u32x2 each)
+
 struct Layout {
-    size_t w, u, qd, kdt, pb, decay, total;
+    size_t w, qd, kd, pb, u, decay, total;
     Layout(int T, int H) {
         const size_t NC = (size_t)((T + C - 1) / C), n = (size_t)H * NC;
         size_t at = 0;
@@ -56,11 +76,11 @@ struct Layout {
             at = (at + bytes + 255) / 256 * 256;
             return off;
         };
-        w = take(n * C * DK * 2);
-        u = take(n * C * DK * 2);
-        qd = take(n * C * DK * 2);
-        kdt = take(n * C * DK * 2);
-        pb = take(n * C * C * 2);
+        w = take(n * 16 * 1024);
+        qd = take(n * 16 * 1024);
+        kd = take(n * 16 * 1024);
+        pb = take(n * 8 * 1024);
+        u = take(n * 32 * 512);
         decay = take(n * 4);
         total = at;
     }
@@ -69,9 +89,9 @@ struct Layout {
 Work split(float* workspace, int T, int H) {
     const Layout l(T, H);
     unsigned char* b = reinterpret_cast<unsigned char*>(workspace);
-    return Work{reinterpret_cast<bf16*>(b + l.w),   reinterpret_cast<bf16*>(b + l.u),
-                reinterpret_cast<bf16*>(b + l.qd),  reinterpret_cast<bf16*>(b + l.kdt),
-                reinterpret_cast<bf16*>(b + l.pb),  reinterpret_cast<float*>(b + l.decay)};
+    return Work{reinterpret_cast<u32x4*>(b + l.w),  reinterpret_cast<u32x4*>(b + l.qd),
+                reinterpret_cast<u32x4*>(b + l.kd), reinterpret_cast<u32x4*>(b + l.pb),
+                reinterpret_cast<u32x2*>(b + l.u),  reinterpret_cast<float*>(b + l.decay)};
 }
 
 // cvt.rna.tf32.f32: 10 explicit mantissa bits, round half away from zero.
@@ -81,170 +101,262 @@ __device__ __forceinline__ float tf32_rna(float x) {
     return __uint_as_float(u);
 }
 
-__device__ __forceinline__ u32x4 ld16(const bf16* p) {
-    const Pack8 v = *reinterpret_cast<const Pack8*>(p);
-    return u32x4{v.w[0], v.w[1], v.w[2], v.w[3]};
+// 8 bf16 of a row in the permuted k order of lane group g: k = 32 s + {4g..4g+3, 16+4g..}
+__device__ __forceinline__ u32x4 load_perm(const bf16* row, int s, int g, bool valid) {
+    if (!valid) return u32x4{0u, 0u, 0u, 0u};
+    const u32x2 a = *reinterpret_cast<const u32x2*>(row + 32 * s + 4 * g);
+    const u32x2 b = *reinterpret_cast<const u32x2*>(row + 32 * s + 16 + 4 * g);
+    return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+__device__ __forceinline__ void unpack8v(const u32x4& p, float out[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        out[2 * i] = lo_f32(p[i]);
+        out[2 * i + 1] = hi_f32(p[i]);
+    }
+}
+
+__device__ __forceinline__ u32x4 pack8v(const float x[8]) {
+    return u32x4{pack2(x[0], x[1]), pack2(x[2], x[3]), pack2(x[4], x[5]), pack2(x[6], x[7])};
+}
+
+// two accumulator tiles (rows 4g + r of tile 0 and of tile 1) as one operand in perm order
+__device__ __forceinline__ u32x4 pack_pair(const f32x4& t0, const f32x4& t1) {
+    return u32x4{pack2(t0[0], t0[1]), pack2(t0[2], t0[3]), pack2(t1[0], t1[1]), pack2(t1[2], t1[3])};
+}
+
+// B operand selecting k = 16 half + (l % 16) in perm order: D = A B copies 16 columns of A.
+__device__ __forceinline__ u32x4 select_op(int half, int col, int grp) {
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+    const int d = col - 4 * grp;  // position within the lane group's run of four
+    if (d >= 0 && d < 4) {
+        const int e = d + 4 * half;
+        v[e >> 1] = BF16_ONE << (16 * (e & 1));
+    }
+    return u32x4{v[0], v[1], v[2], v[3]};
+}
+
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
 // ------------------------------------------------------------------ gdn_prep
 
-constexpr int PT = 512;          // threads
-constexpr int PW = PT / 64;      // waves
-constexpr int PLD = DK + 8;      // bf16 stride of the split planes [64][128]
-constexpr int TLD = C + 8;       // bf16 stride of [128][64] transposes and of Tb [64][64]
-constexpr int FLD = C + 1;       // float stride of A and T [64][64]
+constexpr int PT = 256;          // threads, 4 waves
+constexpr int FLD = C + 1;       // float stride of A and T [64][65]
+constexpr int TLD = C + 8;       // bf16 stride of Tb [64][72]
 
-// LDS map (bytes). Region 0 holds the four split planes during the pair products, then
-// T (float), the level scratch, Tb (bf16) and v^T (bf16).
-constexpr int PLANE = C * PLD * 2;                 // 17408
-constexpr int R0 = 0;                              // 4 planes: k hi, k lo, q hi, q lo
-constexpr int R0_TM = 0;                           // T float [64][65]
-constexpr int R0_SC = R0_TM + C * FLD * 4;         // level scratch float [3][256]
-constexpr int R0_TB = R0_SC + 3 * 256 * 4;         // Tb bf16 [64][72]
-constexpr int R0_VT = R0_TB + C * TLD * 2;         // v^T bf16 [128][72]
-constexpr int R1 = R0 + 4 * PLANE;                 // kw^T bf16 [128][72]
-constexpr int R2 = R1 + DK * TLD * 2;              // kd^T bf16 [128][72]
-constexpr int R3 = R2 + DK * TLD * 2;              // A float [64][65]
-constexpr int R4 = R3 + C * FLD * 4;               // cum, beta, e^cum, e^(last-cum)
-constexpr int PREP_SMEM = R4 + 4 * C * 4;
-static_assert(R0_VT + DK * TLD * 2 <= R1, "region 0 overlay fits");
+// LDS map (bytes). Region 0: split planes of k^ in fragment order during the pair
+// products; afterwards T (float), Tb (bf16) and a per-wave 16x16 float scratch.
+constexpr int R0 = 0;
+constexpr int PLANE = 4 * 4 * 1024;                // [4 blocks][4 steps] fragments
+constexpr int R0_TM = 0;
+constexpr int R0_TB = R0_TM + C * FLD * 4;         // 16640
+constexpr int R0_SC = R0_TB + C * TLD * 2;         // 25856
+constexpr int R1 = R0 + 2 * PLANE;                 // A float [64][65]
+constexpr int R2 = R1 + C * FLD * 4;               // cum, beta, e^cum, e^(last-cum), k inverse norm
+constexpr int PREP_SMEM = R2 + 5 * C * 4;
+static_assert(R0_SC + 4 * 256 * 4 <= R1, "region 0 overlay fits");
+
+#ifdef Q35_PHASE_TIMING
+// Development aid: per-phase shader-clock ticks summed over all blocks.
+__device__ unsigned long long q35_phase_ticks[16];
+#define Q35_PHASE_START() uint64_t q35_t0 = __builtin_amdgcn_s_memtime()
+#define Q35_PHASE(i)                                                             \
+    do {                                                                         \
+        const uint64_t q35_t1 = __builtin_amdgcn_s_memtime();                    \
+        if (threadIdx.x == 0) atomicAdd(&q35_phase_ticks[i], q35_t1 - q35_t0);   \
+        q35_t0 = q35_t1;                                                         \
+    } while (0)
+#define Q35_LPHASE_START() uint64_t q35_t0 = __builtin_amdgcn_s_memtime(), q35_acc[5] = {0, 0, 0, 0, 0}
+#define Q35_LPHASE(i)                                          \
+    do {                                                       \
+        const uint64_t q35_t1 = __builtin_amdgcn_s_memtime();  \
+        q35_acc[(i) - 8] += q35_t1 - q35_t0;                   \
+        q35_t0 = q35_t1;                                       \
+    } while (0)
+#define Q35_LPHASE_FLUSH()                                                                             \
+    do {                                                                                               \
+        if (threadIdx.x == 0)                                                                          \
+            for (int q35_i = 0; q35_i < 5; q35_i++) atomicAdd(&q35_phase_ticks[8 + q35_i], q35_acc[q35_i]); \
+    } while (0)
+#else
+#define Q35_PHASE_START() (void)0
+#define Q35_PHASE(i) (void)0
+#define Q35_LPHASE_START() (void)0
+#define Q35_LPHASE(i) (void)0
+#define Q35_LPHASE_FLUSH() (void)0
+#endif
 
 __global__ void __launch_bounds__(PT)
     gdn_prep(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
              const float* __restrict__ g, const bf16* __restrict__ beta, Work ws, int T, int H, int HK, float scale) {
     extern __shared__ __align__(16) unsigned char sm[];
-    bf16* khi = reinterpret_cast<bf16*>(sm + R0);
-    bf16* klo = khi + C * PLD;
-    bf16* qhi = klo + C * PLD;
-    bf16* qlo = qhi + C * PLD;
+    u32x4* khi_pl = reinterpret_cast<u32x4*>(sm + R0);
+    u32x4* klo_pl = reinterpret_cast<u32x4*>(sm + R0 + PLANE);
     float* tm = reinterpret_cast<float*>(sm + R0_TM);
-    float* sc = reinterpret_cast<float*>(sm + R0_SC);
     bf16* tb = reinterpret_cast<bf16*>(sm + R0_TB);
-    bf16* vt = reinterpret_cast<bf16*>(sm + R0_VT);
-    bf16* kwt = reinterpret_cast<bf16*>(sm + R1);
-    bf16* kdt = reinterpret_cast<bf16*>(sm + R2);
-    float* am = reinterpret_cast<float*>(sm + R3);
-    float* cum = reinterpret_cast<float*>(sm + R4);
+    float* am = reinterpret_cast<float*>(sm + R1);
+    float* cum = reinterpret_cast<float*>(sm + R2);
     float* bet = cum + C;
     float* ecum = bet + C;
     float* erem = ecum + C;
+    float* kinv_s = erem + C;
 
     const int c = blockIdx.x, h = blockIdx.y, NC = gridDim.x;
     const int hk = h / (H / HK);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
+    float* scr = reinterpret_cast<float*>(sm + R0_SC) + wave * 256;
     const size_t rec = (size_t)h * NC + c;
+    const int t0 = c * C;
+    Q35_PHASE_START();
 
-    // 1. cumulative log-decay: lane i of wave 0 sums g_0 .. g_i in index order
+    // 0. loads: own k rows (block `wave`), q rows (block 3 - wave), and the k and v columns
+    //    of dim step `wave` for all 64 tokens; gates for all tokens (lane = token)
+    const int qb = 3 - wave;
+    const int krow = 16 * wave + col, qrow = 16 * qb + col;
+    u32x4 kraw[4], qraw[4], kc[4], vc[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        kraw[s] = load_perm(k + ((size_t)(t0 + krow) * HK + hk) * DK, s, grp, t0 + krow < T);
+        qraw[s] = load_perm(q + ((size_t)(t0 + qrow) * HK + hk) * DK, s, grp, t0 + qrow < T);
+    }
+#pragma unroll
+    for (int tb_ = 0; tb_ < 4; tb_++) {
+        const int t = t0 + 16 * tb_ + col;
+        kc[tb_] = load_perm(k + ((size_t)t * HK + hk) * DK, wave, grp, t < T);
+        vc[tb_] = load_perm(v + ((size_t)t * H + h) * DK, wave, grp, t < T);
+    }
+    const int tl = t0 + lane;
+    const float gv = tl < T ? g[(size_t)tl * H + h] : 0.f;
+    const float bv = tl < T ? f32(beta[(size_t)tl * H + h]) : 0.f;
+
+    // 1. cumulative log-decay, in index order (every wave, lane = token)
+    float cs = 0.f;
+    for (int j = 0; j < C; j++) {
+        const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
+        if (j <= lane) cs = cs + gj;
+    }
+    const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs), C - 1));
+    const float ec = expf(cs), er = expf(last - cs);
     if (wave == 0) {
-        const int t = c * C + lane;
-        const float gv = t < T ? g[(size_t)t * H + h] : 0.f;
-        bet[lane] = t < T ? f32(beta[(size_t)t * H + h]) : 0.f;
-        float s = 0.f;
-        for (int j = 0; j < C; j++) {
-            const float gj = __shfl(gv, j, 64);
-            if (j <= lane) s = s + gj;
-        }
-        cum[lane] = s;
-        const float last = __shfl(s, C - 1, 64);
-        ecum[lane] = expf(s);
-        erem[lane] = expf(last - s);
-        if (lane == C - 1) ws.decay[rec] = expf(s);
+        cum[lane] = cs;
+        bet[lane] = bv;
+        ecum[lane] = ec;
+        erem[lane] = er;
+        if (lane == C - 1) ws.decay[rec] = expf(cs);
     }
-    __syncthreads();
+    Q35_PHASE(1);
 
-    // 2. L2 norms (16 lanes x 8 dims per row), TF32 split planes, qd, kw^T, kd^T
-    for (int r0 = 0; r0 < C; r0 += PT / 16) {
-        const int r = r0 + tid / 16, sub = tid & 15, d0 = sub * 8;
-        const int t = c * C + r;
-        float kv[8], qv[8];
-        if (t < T) {
-            unpack8(*reinterpret_cast<const Pack8*>(k + ((size_t)t * HK + hk) * DK + d0), kv);
-            unpack8(*reinterpret_cast<const Pack8*>(q + ((size_t)t * HK + hk) * DK + d0), qv);
-        } else {
+    // 2. L2 norms (row sums over the 4 lane groups), TF32 split of k^, q^ and qd
+    float ks = 0.f, qs = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) kv[e] = qv[e] = 0.f;
-        }
-        float ks = 0.f, qs = 0.f;
+    for (int s = 0; s < 4; s++) {
+        float kf[8], qf[8];
+        unpack8v(kraw[s], kf);
+        unpack8v(qraw[s], qf);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            ks += kv[e] * kv[e];
-            qs += qv[e] * qv[e];
+            ks += kf[e] * kf[e];
+            qs += qf[e] * qf[e];
         }
-        ks = lane_sum<16>(ks);
-        qs = lane_sum<16>(qs);
-        const float kinv = rsqrtf(ks + 1e-6f), qinv = rsqrtf(qs + 1e-6f) * scale;
-        float khv[8], klv[8], qhv[8], qlv[8], qdv[8];
+    }
+    ks += __shfl_xor(ks, 16, 64);
+    ks += __shfl_xor(ks, 32, 64);
+    qs += __shfl_xor(qs, 16, 64);
+    qs += __shfl_xor(qs, 32, 64);
+    const float kinv = rsqrtf(ks + 1e-6f), qinv = rsqrtf(qs + 1e-6f) * scale;
+    if (grp == 0) kinv_s[krow] = kinv;
+    const float ecq = __shfl(ec, qrow, 64);
+    u32x4 khi[4], klo[4], qhi[4], qlo[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        float hk_[8], lk_[8], hq_[8], lq_[8], qd_[8], kf[8], qf[8];
+        unpack8v(kraw[s], kf);
+        unpack8v(qraw[s], qf);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const float kx = kv[e] * kinv, qx = qv[e] * qinv;
-            const float kt = tf32_rna(kx), qt = tf32_rna(qx);
-            khv[e] = round_bf16(kt);
-            klv[e] = kt - khv[e];
-            qhv[e] = round_bf16(qt);
-            qlv[e] = qt - qhv[e];
-            qdv[e] = qx * ecum[r];
-            kwt[(d0 + e) * TLD + r] = to_bf16(kx * ecum[r]);
-            kdt[(d0 + e) * TLD + r] = to_bf16(kx * erem[r]);
+            const float kt = tf32_rna(kf[e] * kinv);
+            hk_[e] = round_bf16(kt);
+            lk_[e] = kt - hk_[e];
+            const float qx = qf[e] * qinv;
+            const float qt = tf32_rna(qx);
+            hq_[e] = round_bf16(qt);
+            lq_[e] = qt - hq_[e];
+            qd_[e] = qx * ecq;
         }
-        *reinterpret_cast<Pack8*>(khi + r * PLD + d0) = pack8(khv);
-        *reinterpret_cast<Pack8*>(klo + r * PLD + d0) = pack8(klv);
-        *reinterpret_cast<Pack8*>(qhi + r * PLD + d0) = pack8(qhv);
-        *reinterpret_cast<Pack8*>(qlo + r * PLD + d0) = pack8(qlv);
-        *reinterpret_cast<Pack8*>(ws.qd + (rec * C + r) * DK + d0) = pack8(qdv);
+        khi[s] = pack8v(hk_);
+        klo[s] = pack8v(lk_);
+        qhi[s] = pack8v(hq_);
+        qlo[s] = pack8v(lq_);
+        khi_pl[(wave * 4 + s) * FRAG + lane] = khi[s];
+        klo_pl[(wave * 4 + s) * FRAG + lane] = klo[s];
+        ws.qd[(rec * 16 + qb * 4 + s) * FRAG + lane] = pack8v(qd_);
     }
     __syncthreads();
+    Q35_PHASE(2);
 
-    // kd^T to the workspace, 16-byte stores
-    for (int x = tid; x < DK * C / 8; x += PT) {
-        const int d = x / (C / 8), j0 = (x % (C / 8)) * 8;
-        *reinterpret_cast<Pack8*>(ws.kdt + (rec * DK + d) * C + j0) = *reinterpret_cast<const Pack8*>(kdt + d * TLD + j0);
-    }
-
-    // 3. pair products on the lower 16x16 tiles: e < 10 -> k.k (A), else q.k (P)
-    bf16* pbg = ws.pb + rec * C * C;
-    for (int e = wave; e < 20; e += PW) {
-        const int tile = e % 10;
-        const int it = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
-        const int jt = tile - it * (it + 1) / 2;
-        const bf16* ah = e < 10 ? khi : qhi;
-        const bf16* al = e < 10 ? klo : qlo;
+    // 3. pair products. A tiles (wave, jt <= wave): rows i of this wave's k^, columns j.
+#pragma unroll
+    for (int jt = 0; jt < 4; jt++) {
+        if (jt > wave) continue;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < DK / 32; s++) {
-            const int ao = (16 * it + col) * PLD + 32 * s + 8 * grp;
-            const int bo = (16 * jt + col) * PLD + 32 * s + 8 * grp;
-            const u32x4 a_h = ld16(ah + ao), a_l = ld16(al + ao);
-            const u32x4 b_h = ld16(khi + bo), b_l = ld16(klo + bo);
-            acc = mfma16(a_l, b_l, acc);
-            acc = mfma16(a_l, b_h, acc);
-            acc = mfma16(a_h, b_l, acc);
-            acc = mfma16(a_h, b_h, acc);
+        for (int s = 0; s < 4; s++) {
+            const u32x4 bh = khi_pl[(jt * 4 + s) * FRAG + lane], bl = klo_pl[(jt * 4 + s) * FRAG + lane];
+            acc = mfma16(klo[s], bl, acc);
+            acc = mfma16(klo[s], bh, acc);
+            acc = mfma16(khi[s], bl, acc);
+            acc = mfma16(khi[s], bh, acc);
         }
         const int j = 16 * jt + col;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int i = 16 * it + 4 * grp + r;
+            const int i = 16 * wave + 4 * grp + r;
             const float dec = j <= i ? expf(cum[i] - cum[j]) : 0.f;
-            if (e < 10)
-                am[i * FLD + j] = j < i ? bet[i] * acc[r] * dec : 0.f;
-            else
-                pbg[i * C + j] = j <= i ? to_bf16(acc[r] * dec) : (bf16)0;
+            am[i * FLD + j] = j < i ? bet[i] * acc[r] * dec : 0.f;
         }
     }
-    // the six tiles above the diagonal of pb are zero
-    for (int x = tid; x < 6 * 256; x += PT) {
-        const int tile = x / 256, r = (x % 256) / 16, cc = x % 16;
-        const int it = tile < 3 ? 0 : tile < 5 ? 1 : 2;
-        const int jt = tile < 3 ? tile + 1 : tile < 5 ? tile - 1 : 3;
-        pbg[(16 * it + r) * C + 16 * jt + cc] = 0;
+    // P^T tiles (jt <= qb, qb): rows j of k^ (planes), columns i of this wave's q^ rows.
+    // pb fragment (qb, s) = tiles 2s and 2s + 1, lane for lane.
+    {
+        f32x4 pt[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; jt++) {
+            pt[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (jt > qb) continue;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const u32x4 ah = khi_pl[(jt * 4 + s) * FRAG + lane], al = klo_pl[(jt * 4 + s) * FRAG + lane];
+                pt[jt] = mfma16(al, qlo[s], pt[jt]);
+                pt[jt] = mfma16(al, qhi[s], pt[jt]);
+                pt[jt] = mfma16(ah, qlo[s], pt[jt]);
+                pt[jt] = mfma16(ah, qhi[s], pt[jt]);
+            }
+            const int i = qrow;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = 16 * jt + 4 * grp + r;
+                pt[jt][r] = j <= i ? round_bf16(pt[jt][r] * expf(cum[i] - cum[j])) : 0.f;
+            }
+        }
+        ws.pb[(rec * 8 + qb * 2 + 0) * FRAG + lane] = pack_pair(pt[0], pt[1]);
+        ws.pb[(rec * 8 + qb * 2 + 1) * FRAG + lane] = pack_pair(pt[2], pt[3]);
     }
     __syncthreads();
+    Q35_PHASE(3);
 
-    // 4. T = (I + A)^-1: 16x16 diagonal blocks by forward substitution, then three levels
-    for (int x = tid; x < C * FLD; x += PT) tm[x] = 0.f;
-    __syncthreads();
-    if (tid < C) {
-        const int base = 16 * (tid / 16), cc = tid % 16;
+    // 4. T = (I + A)^-1. Upper off-diagonal blocks are zero; the diagonal blocks by forward
+    //    substitution in the reference order (wave w, lanes 0..15: one column each).
+    for (int x = tid; x < 6 * 256; x += PT) {
+        const int blk = x / 256, r = (x % 256) / 16, cc = x % 16;
+        const int bi = blk < 3 ? 0 : blk < 5 ? 1 : 2;
+        const int bj = blk < 3 ? blk + 1 : blk < 5 ? blk - 1 : 3;
+        tm[(16 * bi + r) * FLD + 16 * bj + cc] = 0.f;
+    }
+    if (lane < 16) {
+        const int base = 16 * wave, cc = lane;
         float xs[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -257,59 +369,101 @@ __global__ void __launch_bounds__(PT)
         for (int r = 0; r < 16; r++) tm[(base + r) * FLD + base + cc] = xs[r];
     }
     __syncthreads();
+    Q35_PHASE(4);
+    //    levels: wave bi computes T_{bi, bi - lv} = -T_ii (sum_k A_ik T_kj) on the f32 MFMA
+    //    (A operand: lane = row l%16, k = l/16; B operand: lane = column l%16, k = l/16)
     for (int lv = 1; lv < 4; lv++) {
-        const int nb = 4 - lv;
-        for (int x = tid; x < nb * 256; x += PT) {
-            const int bi = lv + x / 256, bj = bi - lv, r = (x % 256) / 16, cc = x % 16;
-            float acc = 0.f;
+        const int bi = wave, bj = wave - lv;
+        const bool active = bj >= 0;
+        if (active) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             for (int kb = bj; kb < bi; kb++)
 #pragma unroll
-                for (int m = 0; m < 16; m++)
-                    acc = fmaf(am[(16 * bi + r) * FLD + 16 * kb + m], tm[(16 * kb + m) * FLD + 16 * bj + cc], acc);
-            sc[x] = acc;
+                for (int kk = 0; kk < 4; kk++)
+                    acc = mfma_f32(am[(16 * bi + col) * FLD + 16 * kb + 4 * kk + grp],
+                                   tm[(16 * kb + 4 * kk + grp) * FLD + 16 * bj + col], acc);
+#pragma unroll
+            for (int r = 0; r < 4; r++) scr[(4 * grp + r) * 16 + col] = acc[r];
         }
         __syncthreads();
-        for (int x = tid; x < nb * 256; x += PT) {
-            const int bi = lv + x / 256, bj = bi - lv, r = (x % 256) / 16, cc = x % 16;
-            const float* s0 = sc + (x / 256) * 256 + cc;
-            float acc = 0.f;
-            for (int m = 0; m <= r; m++) acc = fmaf(tm[(16 * bi + r) * FLD + 16 * bi + m], s0[m * 16], acc);
-            tm[(16 * bi + r) * FLD + 16 * bj + cc] = -acc;
+        if (active) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+                acc = mfma_f32(tm[(16 * bi + col) * FLD + 16 * bi + 4 * kk + grp], scr[(4 * kk + grp) * 16 + col], acc);
+#pragma unroll
+            for (int r = 0; r < 4; r++) tm[(16 * bi + 4 * grp + r) * FLD + 16 * bj + col] = -acc[r];
         }
         __syncthreads();
     }
+    Q35_PHASE(5);
 
-    // 5. Tb = bf16(T beta_j); v^T; then u = Tb v and w = Tb kw on the MFMA
+    // 5. Tb = bf16(T beta_j)
     for (int x = tid; x < C * C; x += PT) {
         const int i = x / C, j = x % C;
         tb[i * TLD + j] = to_bf16(tm[i * FLD + j] * bet[j]);
     }
-    for (int x = tid; x < C * DK / 8; x += PT) {
-        const int j = x / (DK / 8), d0 = (x % (DK / 8)) * 8;
-        const int t = c * C + j;
-        Pack8 p = Pack8{{0u, 0u, 0u, 0u}};
-        if (t < T) p = *reinterpret_cast<const Pack8*>(v + ((size_t)t * H + h) * DK + d0);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            vt[(d0 + 2 * e) * TLD + j] = (bf16)(p.w[e] & 0xffffu);
-            vt[(d0 + 2 * e + 1) * TLD + j] = (bf16)(p.w[e] >> 16);
-        }
-    }
     __syncthreads();
-    for (int e = wave; e < 64; e += PW) {
-        const bool is_u = e < 32;
-        const int it = (e % 32) / 8, dt = e % 8;
-        const bf16* bsrc = is_u ? vt : kwt;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s <= it / 2; s++) {  // T is lower triangular
-            const u32x4 a = ld16(tb + (16 * it + col) * TLD + 32 * s + 8 * grp);
-            const u32x4 b = ld16(bsrc + (16 * dt + col) * TLD + 32 * s + 8 * grp);
-            acc = mfma16(a, b, acc);
-        }
-        bf16* dst = (is_u ? ws.u : ws.w) + rec * C * DK + 16 * dt + col;
+    Q35_PHASE(6);
+
+    // 6. dims 32 wave .. 32 wave + 31: kw, kd and v transposed on the MFMA (lane = dim,
+    //    4 tokens per tile), then kd^T fragments, u = Tb v tiles and w^T = kw^T Tb^T tiles.
+    //    Operand fk[s][half] = kw^T fragment (dims 16 (2 wave + half) + l%16, tokens step s);
+    //    fv likewise for v.
+    u32x4 fkw[2][2], fvt[2][2];
 #pragma unroll
-        for (int r = 0; r < 4; r++) dst[(16 * it + 4 * grp + r) * DK] = to_bf16(acc[r]);
+    for (int s = 0; s < 2; s++) {
+        f32x4 tkw[2][2], tkd[2][2], tv[2][2];
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int tb_ = 2 * s + p, row = 16 * tb_ + col;
+            const float ki = kinv_s[row], e1 = ecum[row], e2 = erem[row];
+            float kf[8], a1[8], a2[8];
+            unpack8v(kc[tb_], kf);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float kx = kf[e] * ki;
+                a1[e] = kx * e1;
+                a2[e] = kx * e2;
+            }
+            const u32x4 akw = pack8v(a1), akd = pack8v(a2);
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const u32x4 sel = select_op(half, col, grp);
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                tkw[p][half] = mfma16(akw, sel, z);
+                tkd[p][half] = mfma16(akd, sel, z);
+                tv[p][half] = mfma16(vc[tb_], sel, z);
+            }
+        }
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            ws.kd[(rec * 16 + (2 * wave + half) * 2 + s) * FRAG + lane] = pack_pair(tkd[0][half], tkd[1][half]);
+            fkw[s][half] = pack_pair(tkw[0][half], tkw[1][half]);
+            fvt[s][half] = pack_pair(tv[0][half], tv[1][half]);
+        }
     }
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+        f32x4 wt[2];
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            f32x4 ua = {0.f, 0.f, 0.f, 0.f}, wa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s <= it / 2; s++) {  // T is lower triangular
+                const bf16* tr = tb + (16 * it + col) * TLD + 32 * s + 4 * grp;
+                const u32x2 t_lo = *reinterpret_cast<const u32x2*>(tr);
+                const u32x2 t_hi = *reinterpret_cast<const u32x2*>(tr + 16);
+                const u32x4 tbf = u32x4{t_lo[0], t_lo[1], t_hi[0], t_hi[1]};
+                ua = mfma16(tbf, fvt[s][half], ua);
+                wa = mfma16(fkw[s][half], tbf, wa);
+            }
+            ws.u[(rec * 32 + it * 8 + 2 * wave + half) * FRAG + lane] = u32x2{pack2(ua[0], ua[1]), pack2(ua[2], ua[3])};
+            wt[half] = wa;
+        }
+        ws.w[(rec * 16 + it * 4 + wave) * FRAG + lane] = pack_pair(wt[0], wt[1]);
+    }
+    Q35_PHASE(7);
 }
 
 // ------------------------------------------------------------------ gdn_scan
@@ -321,36 +475,37 @@ constexpr int SLD = DK + 8;  // bf16 stride of Sb^T [16][128]
 constexpr int VLD = C + 8;   // bf16 stride of v_new^T [16][64]
 
 struct ChunkOps {
-    u32x4 w[4];    // w rows 16 wave + col, dims 32 s + 8 grp
-    u32x4 qd[4];   // qd rows, same layout
-    u32x4 pb[2];   // pb rows, tokens 32 s + 8 grp
-    u32x4 kd[2][2];// kd^T rows 32 wave + 16 i + col, tokens 32 s + 8 grp
-    bf16 u[4];     // u rows 16 wave + 4 grp + r, column v0 + col
+    u32x4 w[4];     // w fragments (row block = wave, dim steps)
+    u32x4 qd[4];    // qd fragments
+    u32x4 pb[2];    // pb fragments (row block = wave, token steps)
+    u32x4 kd[2][2]; // kd^T fragments (dim blocks 2 wave + i, token steps)
+    u32x2 u;        // u tile (row block = wave, dim block = slice)
     float decay;
 };
 
-__device__ __forceinline__ void load_chunk(ChunkOps& op, const Work& ws, size_t rec, int wave, int col, int grp,
-                                           int v0) {
-    const bf16* wr = ws.w + (rec * C + 16 * wave + col) * DK + 8 * grp;
-    const bf16* qr = ws.qd + (rec * C + 16 * wave + col) * DK + 8 * grp;
+__device__ __forceinline__ void load_chunk(ChunkOps& op, const Work& ws, size_t rec, int wave, int lane,
+                                           int slice) {
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-        op.w[s] = ld16(wr + 32 * s);
-        op.qd[s] = ld16(qr + 32 * s);
+        op.w[s] = ws.w[(rec * 16 + wave * 4 + s) * FRAG + lane];
+        op.qd[s] = ws.qd[(rec * 16 + wave * 4 + s) * FRAG + lane];
     }
-    const bf16* pr = ws.pb + (rec * C + 16 * wave + col) * C + 8 * grp;
-    op.pb[0] = ld16(pr);
-    op.pb[1] = ld16(pr + 32);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const bf16* kr = ws.kdt + (rec * DK + 32 * wave + 16 * i + col) * C + 8 * grp;
-        op.kd[i][0] = ld16(kr);
-        op.kd[i][1] = ld16(kr + 32);
-    }
-    const bf16* ur = ws.u + (rec * C + 16 * wave + 4 * grp) * DK + v0 + col;
+    for (int s = 0; s < 2; s++) op.pb[s] = ws.pb[(rec * 8 + wave * 2 + s) * FRAG + lane];
 #pragma unroll
-    for (int r = 0; r < 4; r++) op.u[r] = ur[r * DK];
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int s = 0; s < 2; s++) op.kd[i][s] = ws.kd[(rec * 16 + (2 * wave + i) * 2 + s) * FRAG + lane];
+    op.u = ws.u[(rec * 32 + wave * 8 + slice) * FRAG + lane];
     op.decay = ws.decay[rec];
+}
+
+// B operand from a [16][ld] bf16 LDS array: row `col`, k step s in perm order
+__device__ __forceinline__ u32x4 lds_perm(const bf16* base, int ld, int col, int s, int grp) {
+    const bf16* p = base + col * ld + 32 * s + 4 * grp;
+    const u32x2 a = *reinterpret_cast<const u32x2*>(p);
+    const u32x2 b = *reinterpret_cast<const u32x2*>(p + 16);
+    return u32x4{a[0], a[1], b[0], b[1]};
 }
 
 __global__ void __launch_bounds__(ST)
@@ -370,32 +525,37 @@ __global__ void __launch_bounds__(ST)
             st[i][r] = s_in ? s_in[((size_t)h * DK + 32 * wave + 16 * i + 4 * grp + r) * DK + v0 + col] : 0.f;
     }
 
-    ChunkOps cur, nxt;
-    load_chunk(cur, ws, (size_t)h * NC, wave, col, grp, v0);
-    for (int c = 0; c < NC; c++) {
-        if (c + 1 < NC) load_chunk(nxt, ws, (size_t)h * NC + c + 1, wave, col, grp, v0);
+    Q35_LPHASE_START();
+    // one chunk of the scan with its operands already in registers
+    auto step = [&](const ChunkOps& cur, int c) {
         // 1. bf16(S)^T to LDS
 #pragma unroll
         for (int i = 0; i < 2; i++)
             *reinterpret_cast<u32x2*>(sbt + col * SLD + 32 * wave + 16 * i + 4 * grp) =
                 u32x2{pack2(st[i][0], st[i][1]), pack2(st[i][2], st[i][3])};
+        Q35_LPHASE(8);
         __syncthreads();
+        Q35_LPHASE(9);
         // 2. v_new = bf16(u - w Sb) and qd Sb for rows 16 wave ..
         f32x4 ws_acc = {0.f, 0.f, 0.f, 0.f}, oacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            const u32x4 b = ld16(sbt + col * SLD + 32 * s + 8 * grp);
+            const u32x4 b = lds_perm(sbt, SLD, col, s, grp);
             ws_acc = mfma16(cur.w[s], b, ws_acc);
             oacc = mfma16(cur.qd[s], b, oacc);
         }
-        float vn[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) vn[r] = f32(cur.u[r]) - ws_acc[r];
-        *reinterpret_cast<u32x2*>(vnt + col * VLD + 16 * wave + 4 * grp) = u32x2{pack2(vn[0], vn[1]), pack2(vn[2], vn[3])};
+        const float vn0 = lo_f32(cur.u[0]) - ws_acc[0], vn1 = hi_f32(cur.u[0]) - ws_acc[1];
+        const float vn2 = lo_f32(cur.u[1]) - ws_acc[2], vn3 = hi_f32(cur.u[1]) - ws_acc[3];
+        *reinterpret_cast<u32x2*>(vnt + col * VLD + 16 * wave + 4 * grp) = u32x2{pack2(vn0, vn1), pack2(vn2, vn3)};
+        Q35_LPHASE(10);
         __syncthreads();
+        Q35_LPHASE(11);
         // 3. o = qd Sb + pb v_new
+        u32x4 vb[2];
 #pragma unroll
-        for (int s = 0; s < 2; s++) oacc = mfma16(cur.pb[s], ld16(vnt + col * VLD + 32 * s + 8 * grp), oacc);
+        for (int s = 0; s < 2; s++) vb[s] = lds_perm(vnt, VLD, col, s, grp);
+#pragma unroll
+        for (int s = 0; s < 2; s++) oacc = mfma16(cur.pb[s], vb[s], oacc);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int t = c * C + 16 * wave + 4 * grp + r;
@@ -406,10 +566,30 @@ __global__ void __launch_bounds__(ST)
         for (int i = 0; i < 2; i++) {
             st[i] *= cur.decay;
 #pragma unroll
-            for (int s = 0; s < 2; s++) st[i] = mfma16(cur.kd[i][s], ld16(vnt + col * VLD + 32 * s + 8 * grp), st[i]);
+            for (int s = 0; s < 2; s++) st[i] = mfma16(cur.kd[i][s], vb[s], st[i]);
         }
-        cur = nxt;
+        Q35_LPHASE(12);
+    };
+
+    // three rotating operand sets: chunk c + 2 is in flight while chunk c runs. Loads are
+    // unconditional (the index is clamped; a repeated last chunk is never used) so that
+    // the compiler counts them and waits only for the set in use.
+    ChunkOps opa, opb, opc;
+    const size_t rec0 = (size_t)h * NC;
+    auto at = [&](int c) { return rec0 + min(c, NC - 1); };
+    load_chunk(opa, ws, at(0), wave, lane, slice);
+    load_chunk(opb, ws, at(1), wave, lane, slice);
+    for (int c = 0; c < NC; c += 3) {
+        load_chunk(opc, ws, at(c + 2), wave, lane, slice);
+        step(opa, c);
+        if (c + 1 >= NC) break;
+        load_chunk(opa, ws, at(c + 3), wave, lane, slice);
+        step(opb, c + 1);
+        if (c + 2 >= NC) break;
+        load_chunk(opb, ws, at(c + 4), wave, lane, slice);
+        step(opc, c + 2);
     }
+    Q35_LPHASE_FLUSH();
     if (s_out) {
 #pragma unroll
         for (int i = 0; i < 2; i++)
@@ -458,6 +638,12 @@ int gdn_run(const void* q, const void* k, const void* v, const float* g, const v
 }  // namespace q35
 
 using namespace q35;
+
+#ifdef Q35_PHASE_TIMING
+extern "C" int q35_debug_phase_ticks(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(q35_phase_ticks), sizeof(q35_phase_ticks));
+}
+#endif
 
 extern "C" size_t cs1_gdn_workspace_floats(int T, int H) {
     if (T < 0 || H < 0) return 0;
