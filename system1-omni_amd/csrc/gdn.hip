@@ -468,36 +468,60 @@ __global__ void __launch_bounds__(PT)
 
 // ------------------------------------------------------------------ gdn_scan
 
-constexpr int ST = 256;   // threads, 4 waves
+constexpr int ST = 512;   // threads: waves 0-3 carry the state, waves 4-7 the output
 constexpr int BV = 16;    // value columns per block
 constexpr int NS = DK / BV;
 constexpr int SLD = DK + 8;  // bf16 stride of Sb^T [16][128]
 constexpr int VLD = C + 8;   // bf16 stride of v_new^T [16][64]
 
-struct ChunkOps {
+struct ChainOps {
     u32x4 w[4];     // w fragments (row block = wave, dim steps)
-    u32x4 qd[4];    // qd fragments
-    u32x4 pb[2];    // pb fragments (row block = wave, token steps)
     u32x4 kd[2][2]; // kd^T fragments (dim blocks 2 wave + i, token steps)
     u32x2 u;        // u tile (row block = wave, dim block = slice)
     float decay;
 };
 
-__device__ __forceinline__ void load_chunk(ChunkOps& op, const Work& ws, size_t rec, int wave, int lane,
-                                           int slice) {
+struct OutOps {
+    u32x4 qd[4];    // qd fragments (row block = wave - 4, dim steps)
+    u32x4 pb[2];    // pb fragments (row block, token steps)
+};
+
+// Fragment streams of one head as raw buffer loads: the descriptor (scalar registers) points
+// at the head's first record, the per-chunk byte offset is a scalar soffset and the lane
+// offset is one fixed vector register, so the loads need no vector address arithmetic
+// (vector address temporaries would alias the destinations of loads still in flight).
+struct Streams {
+    __amdgpu_buffer_rsrc_t w, kd, qd, pb, u;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t stream_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ void load_chain(ChainOps& op, const Streams& sr, const float* decay, int c, int rb,
+                                           int lane, int slice) {
+    const int v16 = lane * 16;
+    const int rec_w = c * 16 * 1024 + rb * 4 * 1024;
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-        op.w[s] = ws.w[(rec * 16 + wave * 4 + s) * FRAG + lane];
-        op.qd[s] = ws.qd[(rec * 16 + wave * 4 + s) * FRAG + lane];
-    }
+    for (int s = 0; s < 4; s++) op.w[s] = bload16(sr.w, v16 + s * 1024, rec_w);
 #pragma unroll
-    for (int s = 0; s < 2; s++) op.pb[s] = ws.pb[(rec * 8 + wave * 2 + s) * FRAG + lane];
+    for (int i = 0; i < 4; i++) op.kd[i >> 1][i & 1] = bload16(sr.kd, v16 + i * 1024, rec_w);
+    const u32x2 uu = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(sr.u, lane * 8, c * 32 * 512 + (rb * 8 + slice) * 512, 0));
+    op.u = uu;
+    op.decay = decay[c];
+}
+
+__device__ __forceinline__ void load_out(OutOps& op, const Streams& sr, int c, int rb, int lane) {
+    const int v16 = lane * 16;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int s = 0; s < 4; s++) op.qd[s] = bload16(sr.qd, v16 + s * 1024, c * 16 * 1024 + rb * 4 * 1024);
 #pragma unroll
-        for (int s = 0; s < 2; s++) op.kd[i][s] = ws.kd[(rec * 16 + (2 * wave + i) * 2 + s) * FRAG + lane];
-    op.u = ws.u[(rec * 32 + wave * 8 + slice) * FRAG + lane];
-    op.decay = ws.decay[rec];
+    for (int s = 0; s < 2; s++) op.pb[s] = bload16(sr.pb, v16 + s * 1024, c * 8 * 1024 + rb * 2 * 1024);
 }
 
 // B operand from a [16][ld] bf16 LDS array: row `col`, k step s in perm order
@@ -508,94 +532,111 @@ __device__ __forceinline__ u32x4 lds_perm(const bf16* base, int ld, int col, int
     return u32x4{a[0], a[1], b[0], b[1]};
 }
 
+// Per chunk, two barriers:  [chain: write bf16(S)^T]  A  [chain: v_new = u - w Sb -> LDS;
+// output: acc = qd Sb]  B  [chain: S = S decay + kd^T v_new; output: o = acc + pb v_new].
+// Chain waves read Sb only between A and B; output waves read v_new after B and are done
+// before the next A, when v_new is rewritten.
 __global__ void __launch_bounds__(ST)
-    gdn_scan(Work ws, bf16* __restrict__ o, int T, int H, int NC, const float* __restrict__ s_in,
-             float* __restrict__ s_out) {
+    gdn_scan(Work ws, const float* __restrict__ decay_all, bf16* __restrict__ o, int T, int H, int NC,
+             const float* __restrict__ s_in, float* __restrict__ s_out) {
     __shared__ __align__(16) bf16 sbt[BV * SLD];
     __shared__ __align__(16) bf16 vnt[BV * VLD];
     const int h = blockIdx.x % H, slice = blockIdx.x / H, v0 = slice * BV;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
-
-    // state rows 32 wave + 16 i + 4 grp + r, column v0 + col
-    f32x4 st[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            st[i][r] = s_in ? s_in[((size_t)h * DK + 32 * wave + 16 * i + 4 * grp + r) * DK + v0 + col] : 0.f;
-    }
-
-    Q35_LPHASE_START();
-    // one chunk of the scan with its operands already in registers
-    auto step = [&](const ChunkOps& cur, int c) {
-        // 1. bf16(S)^T to LDS
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            *reinterpret_cast<u32x2*>(sbt + col * SLD + 32 * wave + 16 * i + 4 * grp) =
-                u32x2{pack2(st[i][0], st[i][1]), pack2(st[i][2], st[i][3])};
-        Q35_LPHASE(8);
-        __syncthreads();
-        Q35_LPHASE(9);
-        // 2. v_new = bf16(u - w Sb) and qd Sb for rows 16 wave ..
-        f32x4 ws_acc = {0.f, 0.f, 0.f, 0.f}, oacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const u32x4 b = lds_perm(sbt, SLD, col, s, grp);
-            ws_acc = mfma16(cur.w[s], b, ws_acc);
-            oacc = mfma16(cur.qd[s], b, oacc);
-        }
-        const float vn0 = lo_f32(cur.u[0]) - ws_acc[0], vn1 = hi_f32(cur.u[0]) - ws_acc[1];
-        const float vn2 = lo_f32(cur.u[1]) - ws_acc[2], vn3 = hi_f32(cur.u[1]) - ws_acc[3];
-        *reinterpret_cast<u32x2*>(vnt + col * VLD + 16 * wave + 4 * grp) = u32x2{pack2(vn0, vn1), pack2(vn2, vn3)};
-        Q35_LPHASE(10);
-        __syncthreads();
-        Q35_LPHASE(11);
-        // 3. o = qd Sb + pb v_new
-        u32x4 vb[2];
-#pragma unroll
-        for (int s = 0; s < 2; s++) vb[s] = lds_perm(vnt, VLD, col, s, grp);
-#pragma unroll
-        for (int s = 0; s < 2; s++) oacc = mfma16(cur.pb[s], vb[s], oacc);
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int t = c * C + 16 * wave + 4 * grp + r;
-            if (t < T) o[((size_t)t * H + h) * DK + v0 + col] = to_bf16(oacc[r]);
-        }
-        // 4. S = S decay + kd^T v_new
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            st[i] *= cur.decay;
-#pragma unroll
-            for (int s = 0; s < 2; s++) st[i] = mfma16(cur.kd[i][s], vb[s], st[i]);
-        }
-        Q35_LPHASE(12);
-    };
-
-    // three rotating operand sets: chunk c + 2 is in flight while chunk c runs. Loads are
-    // unconditional (the index is clamped; a repeated last chunk is never used) so that
-    // the compiler counts them and waits only for the set in use.
-    ChunkOps opa, opb, opc;
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform for the compiler
+    const bool chain = uwave < 4;
+    const int rb = uwave & 3;  // row block: state rows 32 rb .. (chain) / output rows 16 rb .. (output)
     const size_t rec0 = (size_t)h * NC;
-    auto at = [&](int c) { return rec0 + min(c, NC - 1); };
-    load_chunk(opa, ws, at(0), wave, lane, slice);
-    load_chunk(opb, ws, at(1), wave, lane, slice);
-    for (int c = 0; c < NC; c += 3) {
-        load_chunk(opc, ws, at(c + 2), wave, lane, slice);
-        step(opa, c);
-        if (c + 1 >= NC) break;
-        load_chunk(opa, ws, at(c + 3), wave, lane, slice);
-        step(opb, c + 1);
-        if (c + 2 >= NC) break;
-        load_chunk(opb, ws, at(c + 4), wave, lane, slice);
-        step(opc, c + 2);
-    }
-    Q35_LPHASE_FLUSH();
-    if (s_out) {
+    auto at = [&](int c) { return min(c, NC - 1); };
+    const Streams sr{stream_rsrc(ws.w + rec0 * 16 * FRAG), stream_rsrc(ws.kd + rec0 * 16 * FRAG),
+                     stream_rsrc(ws.qd + rec0 * 16 * FRAG), stream_rsrc(ws.pb + rec0 * 8 * FRAG),
+                     stream_rsrc(ws.u + rec0 * 32 * FRAG)};
+    const float* decay = decay_all + rec0;  // read-only kernel argument: scalar loads
+
+    if (chain) {
+        // state rows 32 rb + 16 i + 4 grp + r, column v0 + col
+        f32x4 st[2];
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                s_out[((size_t)h * DK + 32 * wave + 16 * i + 4 * grp + r) * DK + v0 + col] = st[i][r];
+                st[i][r] = s_in ? s_in[((size_t)h * DK + 32 * rb + 16 * i + 4 * grp + r) * DK + v0 + col] : 0.f;
+        Q35_LPHASE_START();
+        auto step = [&](const ChainOps& cur) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                *reinterpret_cast<u32x2*>(sbt + col * SLD + 32 * rb + 16 * i + 4 * grp) =
+                    u32x2{pack2(st[i][0], st[i][1]), pack2(st[i][2], st[i][3])};
+            Q35_LPHASE(8);
+            __syncthreads();  // A
+            Q35_LPHASE(9);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 4; s++) acc = mfma16(cur.w[s], lds_perm(sbt, SLD, col, s, grp), acc);
+            const float vn0 = lo_f32(cur.u[0]) - acc[0], vn1 = hi_f32(cur.u[0]) - acc[1];
+            const float vn2 = lo_f32(cur.u[1]) - acc[2], vn3 = hi_f32(cur.u[1]) - acc[3];
+            *reinterpret_cast<u32x2*>(vnt + col * VLD + 16 * rb + 4 * grp) = u32x2{pack2(vn0, vn1), pack2(vn2, vn3)};
+            Q35_LPHASE(10);
+            __syncthreads();  // B
+            Q35_LPHASE(11);
+            const u32x4 vb0 = lds_perm(vnt, VLD, col, 0, grp), vb1 = lds_perm(vnt, VLD, col, 1, grp);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                st[i] *= cur.decay;
+                st[i] = mfma16(cur.kd[i][0], vb0, st[i]);
+                st[i] = mfma16(cur.kd[i][1], vb1, st[i]);
+            }
+            Q35_LPHASE(12);
+        };
+        ChainOps opa, opb, opc;
+        load_chain(opa, sr, decay, at(0), rb, lane, slice);
+        load_chain(opb, sr, decay, at(1), rb, lane, slice);
+        for (int c = 0; c < NC; c += 3) {
+            load_chain(opc, sr, decay, at(c + 2), rb, lane, slice);
+            step(opa);
+            if (c + 1 >= NC) break;
+            load_chain(opa, sr, decay, at(c + 3), rb, lane, slice);
+            step(opb);
+            if (c + 2 >= NC) break;
+            load_chain(opb, sr, decay, at(c + 4), rb, lane, slice);
+            step(opc);
+        }
+        Q35_LPHASE_FLUSH();
+        if (s_out) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    s_out[((size_t)h * DK + 32 * rb + 16 * i + 4 * grp + r) * DK + v0 + col] = st[i][r];
+        }
+    } else {
+        auto step = [&](const OutOps& cur, int c) {
+            __syncthreads();  // A
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 4; s++) acc = mfma16(cur.qd[s], lds_perm(sbt, SLD, col, s, grp), acc);
+            __syncthreads();  // B
+#pragma unroll
+            for (int s = 0; s < 2; s++) acc = mfma16(cur.pb[s], lds_perm(vnt, VLD, col, s, grp), acc);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = c * C + 16 * rb + 4 * grp + r;
+                if (t < T) o[((size_t)t * H + h) * DK + v0 + col] = to_bf16(acc[r]);
+            }
+        };
+        OutOps opa, opb, opc;
+        load_out(opa, sr, at(0), rb, lane);
+        load_out(opb, sr, at(1), rb, lane);
+        for (int c = 0; c < NC; c += 3) {
+            load_out(opc, sr, at(c + 2), rb, lane);
+            step(opa, c);
+            if (c + 1 >= NC) break;
+            load_out(opa, sr, at(c + 3), rb, lane);
+            step(opb, c + 1);
+            if (c + 2 >= NC) break;
+            load_out(opb, sr, at(c + 4), rb, lane);
+            step(opc, c + 2);
+        }
     }
 }
 
@@ -630,7 +671,7 @@ int gdn_run(const void* q, const void* k, const void* v, const float* g, const v
     gdn_prep<<<dim3(NC, H), PT, PREP_SMEM, st>>>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
                                                  static_cast<const bf16*>(v), g, static_cast<const bf16*>(beta), ws, T,
                                                  H, HK, scale);
-    gdn_scan<<<H * NS, ST, 0, st>>>(ws, static_cast<bf16*>(o), T, H, NC, si, so);
+    gdn_scan<<<H * NS, ST, 0, st>>>(ws, ws.decay, static_cast<bf16*>(o), T, H, NC, si, so);
     return hipGetLastError();
 }
 
