@@ -82,13 +82,16 @@ __global__ void __launch_bounds__(256)
 
 // ---------------------------------------------------------------- flash attention
 
-constexpr int BM = 64, BN = 64, FA_THREADS = 256;
+constexpr int BN = 64;          // keys per tile
+constexpr int QW = 32;          // queries per wave (two 16-query MFMA column tiles)
+constexpr int FA_THREADS = 256; // four waves
 
 template <int D>
 struct FaSmem {
     static constexpr int KLD = D + 8;   // bf16 row stride of K [BN][D]
     static constexpr int VLD = BN + 8;  // bf16 row stride of V^T [D][BN]
-    static constexpr int BYTES = (BN * KLD + D * VLD) * 2;
+    static constexpr int STAGE = BN * KLD + D * VLD;  // bf16 elements per stage
+    static constexpr int BYTES = 2 * STAGE * 2;        // two stages
 };
 
 template <int D>
@@ -96,9 +99,18 @@ struct TileRegs {
     // this thread's share of one K tile and one V tile (16-byte packs)
     static constexpr int KP = BN * D / 8 / FA_THREADS;        // K packs per thread
     static constexpr int VP = BN / 2 * D / 8 / FA_THREADS;    // V key-pairs x 8 dims per thread
-    Pack8 k[KP];
-    Pack8 v[VP][2];
+    u32x4 k[KP];
+    u32x4 v[VP][2];
 };
+
+__device__ __forceinline__ u32x4 ldg16(const bf16* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+// V^T column swizzle: key pair p of row d is stored at pair p ^ 2 ((d / 8) % 16). Groups of
+// four keys stay contiguous (fragment reads are unchanged in shape) while the transposing
+// stores of one wave, which cover rows 8c + 2e for c = 0..15, spread over all 64 banks.
+__device__ __forceinline__ int vt_pair(int d, int pair) { return pair ^ (((d >> 3) & 15) << 1); }
 
 template <int D>
 __device__ __forceinline__ void load_tile(TileRegs<D>& r, const bf16* __restrict__ k, const bf16* __restrict__ v,
@@ -107,22 +119,17 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& r, const bf16* __restrict
 #pragma unroll
     for (int i = 0; i < TileRegs<D>::KP; i++) {
         const int x = tid + i * FA_THREADS;
-        const int row = x / (D / 8), col = (x % (D / 8)) * 8, s = k0 + row;
-        if (s < T)
-            r.k[i] = *reinterpret_cast<const Pack8*>(k + (size_t)s * ldk + col);
-        else
-            r.k[i] = Pack8{{0u, 0u, 0u, 0u}};
+        const int row = x / (D / 8), col = (x % (D / 8)) * 8, s = min(k0 + row, T - 1);
+        r.k[i] = ldg16(k + (size_t)s * ldk + col);
     }
 #pragma unroll
     for (int i = 0; i < TileRegs<D>::VP; i++) {
         const int x = tid + i * FA_THREADS;
-        const int pair = x / (D / 8), col = (x % (D / 8)) * 8, s = k0 + 2 * pair;
+        const int pair = x / (D / 8), col = (x % (D / 8)) * 8;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            if (s + j < T)
-                r.v[i][j] = *reinterpret_cast<const Pack8*>(v + (size_t)(s + j) * ldv + col);
-            else
-                r.v[i][j] = Pack8{{0u, 0u, 0u, 0u}};
+            const int s = min(k0 + 2 * pair + j, T - 1);  // rows past T are masked out
+            r.v[i][j] = ldg16(v + (size_t)s * ldv + col);
         }
     }
 }
@@ -134,7 +141,7 @@ __device__ __forceinline__ void store_tile(const TileRegs<D>& r, bf16* ks, bf16*
     for (int i = 0; i < TileRegs<D>::KP; i++) {
         const int x = tid + i * FA_THREADS;
         const int row = x / (D / 8), col = (x % (D / 8)) * 8;
-        *reinterpret_cast<Pack8*>(ks + row * FaSmem<D>::KLD + col) = r.k[i];
+        *reinterpret_cast<u32x4*>(ks + row * FaSmem<D>::KLD + col) = r.k[i];
     }
 #pragma unroll
     for (int i = 0; i < TileRegs<D>::VP; i++) {
@@ -143,154 +150,245 @@ __device__ __forceinline__ void store_tile(const TileRegs<D>& r, bf16* ks, bf16*
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             // dims col + 2e and col + 2e + 1 of keys 2 pair, 2 pair + 1
-            const uint32_t a = r.v[i][0].w[e], b = r.v[i][1].w[e];
+            const uint32_t a = r.v[i][0][e], b = r.v[i][1][e];
             const uint32_t lo = (a & 0xffffu) | (b << 16);
             const uint32_t hi = (a >> 16) | (b & 0xffff0000u);
-            *reinterpret_cast<uint32_t*>(vt + (col + 2 * e) * FaSmem<D>::VLD + 2 * pair) = lo;
-            *reinterpret_cast<uint32_t*>(vt + (col + 2 * e + 1) * FaSmem<D>::VLD + 2 * pair) = hi;
+            const int d0 = col + 2 * e, d1 = d0 + 1;
+            *reinterpret_cast<uint32_t*>(vt + d0 * FaSmem<D>::VLD + 2 * vt_pair(d0, pair)) = lo;
+            *reinterpret_cast<uint32_t*>(vt + d1 * FaSmem<D>::VLD + 2 * vt_pair(d1, pair)) = hi;
         }
     }
 }
 
-template <int D, bool GATED>
-__global__ void __launch_bounds__(FA_THREADS)
+#ifdef Q35_PHASE_TIMING
+// Development aid: per-phase shader-clock ticks of the tile loop, summed over blocks.
+__device__ unsigned long long q35_fa_ticks[8];
+#define FA_T0() uint64_t fa_t0 = __builtin_amdgcn_s_memtime(), fa_acc[4] = {0, 0, 0, 0}
+#define FA_T(i)                                                 \
+    do {                                                        \
+        const uint64_t fa_t1 = __builtin_amdgcn_s_memtime();    \
+        fa_acc[i] += fa_t1 - fa_t0;                             \
+        fa_t0 = fa_t1;                                          \
+    } while (0)
+#define FA_FLUSH()                                                                                   \
+    do {                                                                                             \
+        if (threadIdx.x == 0) {                                                                      \
+            for (int fa_i = 0; fa_i < 4; fa_i++) atomicAdd(&q35_fa_ticks[fa_i], fa_acc[fa_i]);       \
+            atomicAdd(&q35_fa_ticks[4], (unsigned long long)ntiles);                                 \
+        }                                                                                            \
+    } while (0)
+#else
+#define FA_T0() (void)0
+#define FA_T(i) (void)0
+#define FA_FLUSH() (void)0
+#endif
+
+// Work split. GQA4 (Hq / Hk a multiple of 4): the four waves are four q-heads of one GQA
+// group on the same 32 query rows, so every K/V tile in LDS serves four heads. Otherwise
+// the four waves are four consecutive 32-row blocks of one head.
+template <int D, bool GATED, bool GQA4, int QT>
+__global__ void __launch_bounds__(FA_THREADS, D == 128 ? 2 : 1)
     flash_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int ldv,
                  const bf16* __restrict__ gate, bf16* __restrict__ out, float* __restrict__ lse, int T, int Hq, int Hk,
                  float scale_log2, int q_base) {
     extern __shared__ __align__(16) unsigned char smem[];
-    bf16* ks = reinterpret_cast<bf16*>(smem);
-    bf16* vt = ks + BN * FaSmem<D>::KLD;
-    const int h = blockIdx.y, hk = h / (Hq / Hk);
-    const int q0 = q_base + (gridDim.x - 1 - blockIdx.x) * BM;
+    bf16* stage0 = reinterpret_cast<bf16*>(smem);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int col = lane & 15, grp = lane >> 4;
-    const int qrow = q0 + wave * 16 + col;  // this lane's query
+    constexpr int QWW = 16 * QT;             // query rows per wave
+    const int nrows = GQA4 ? QWW : 4 * QWW;  // query rows per block
+    const int nblk = (T - q_base + nrows - 1) / nrows;
+    const int units = GQA4 ? Hq / 4 : Hq;  // head units per row block
+    const int b = blockIdx.x;
+    const int rblk = nblk - 1 - b / units;  // longest blocks first
+    const int unit = b % units;
+    const int h = GQA4 ? unit * 4 + wave : unit;
+    const int hk = (GQA4 ? unit * 4 : unit) / (Hq / Hk);
+    const int blk_q0 = q_base + rblk * nrows;
+    const int q0 = blk_q0 + (GQA4 ? 0 : wave * QWW);  // this wave's first query
     const bf16* kh = k + (size_t)hk * D;
     const bf16* vh = v + (size_t)hk * D;
     const int ldk = Hk * D;
 
-    // Q^T fragments (B operand): query qrow, dims 32 s + 8 grp .. + 7
+    // Q^T fragments (B operand): query q0 + 16 qt + col, dims 32 s + 8 grp .. + 7
     constexpr int KS = D / 32;
-    u32x4 qf[KS];
-    {
-        const bf16* qr = q + ((size_t)min(qrow, T - 1) * Hq + h) * D + 8 * grp;
+    u32x4 qf[QT][KS];
+#pragma unroll
+    for (int qt = 0; qt < QT; qt++) {
+        const bf16* qr = q + ((size_t)min(q0 + 16 * qt + col, T - 1) * Hq + h) * D + 8 * grp;
 #pragma unroll
         for (int s = 0; s < KS; s++) {
             const Pack8 p = *reinterpret_cast<const Pack8*>(qr + 32 * s);
-            qf[s] = u32x4{p.w[0], p.w[1], p.w[2], p.w[3]};
+            qf[qt][s] = u32x4{p.w[0], p.w[1], p.w[2], p.w[3]};
         }
     }
 
     constexpr int DT = D / 16;
-    f32x4 o[DT];
+    f32x4 o[QT][DT];
 #pragma unroll
-    for (int i = 0; i < DT; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m = -INFINITY, l = 0.f;
+    for (int qt = 0; qt < QT; qt++)
+#pragma unroll
+        for (int i = 0; i < DT; i++) o[qt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m[QT], l[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; qt++) m[qt] = -INFINITY, l[qt] = 0.f;
 
-    const int kv_end = min(T, q0 + BM);
+    const int kv_end = min(T, blk_q0 + nrows);
     const int ntiles = (kv_end + BN - 1) / BN;
     TileRegs<D> regs;
     load_tile<D>(regs, kh, vh, ldk, ldv, 0, T);
+    wait_vm_all();  // Q fragments and tile 0 are in registers
+    store_tile<D>(regs, stage0, stage0 + BN * FaSmem<D>::KLD);
+    if (ntiles > 1) load_tile<D>(regs, kh, vh, ldk, ldv, BN, T);
+    __syncthreads();
+    FA_T0();
     for (int tile = 0; tile < ntiles; tile++) {
         const int k0 = tile * BN;
-        __syncthreads();  // the previous tile is consumed
-        store_tile<D>(regs, ks, vt);
-        __syncthreads();
-        if (tile + 1 < ntiles) load_tile<D>(regs, kh, vh, ldk, ldv, k0 + BN, T);
-
-        // S^T = K Q^T: 4 sub-tiles of 16 keys
-        f32x4 st[4];
+        const bf16* ks = stage0 + (tile & 1) * FaSmem<D>::STAGE;
+        const bf16* vt = ks + BN * FaSmem<D>::KLD;
+        // S^T = K Q^T: 4 sub-tiles of 16 keys x 2 query tiles; each K fragment feeds both
+        f32x4 st[4][QT];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            st[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            #pragma unroll
+            for (int qt = 0; qt < QT; qt++) st[t][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
             const bf16* kr = ks + (16 * t + col) * FaSmem<D>::KLD + 8 * grp;
 #pragma unroll
             for (int s = 0; s < KS; s++) {
                 const Pack8 p = *reinterpret_cast<const Pack8*>(kr + 32 * s);
-                st[t] = mfma16(u32x4{p.w[0], p.w[1], p.w[2], p.w[3]}, qf[s], st[t]);
+                const u32x4 a = u32x4{p.w[0], p.w[1], p.w[2], p.w[3]};
+                #pragma unroll
+                for (int qt = 0; qt < QT; qt++) st[t][qt] = mfma16(a, qf[qt][s], st[t][qt]);
             }
         }
-        // mask, scale, running max
-        float mx = -INFINITY;
+        FA_T(0);
+        u32x4 pf[QT][2];
+        // Only the tiles that reach the diagonal of this wave's rows or past T need the mask
+        // (wave-uniform test); elsewhere every key is visible to every row.
+        const bool masked = k0 + BN - 1 > q0 || k0 + BN > T;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int qt = 0; qt < QT; qt++) {
+            const int qrow = q0 + 16 * qt + col;
+            // running max of the raw scores (scale > 0), over the 4 lanes {q, q+16, q+32, q+48}
+            float mx = -INFINITY;
+            if (masked) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int key = k0 + 16 * t + 4 * grp + r;
-                const float sv = (key <= qrow && key < T) ? st[t][r] * scale_log2 : -INFINITY;
-                st[t][r] = sv;
-                mx = fmaxf(mx, sv);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mn = fmaxf(m, mx);
-        const float base = mn == -INFINITY ? 0.f : mn;
-        const float alpha = exp2f(m - base);
-        m = mn;
-        l *= alpha;
+                for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int i = 0; i < DT; i++) o[i] *= alpha;
-        u32x4 pf[2];
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float p = exp2f(st[t][r] - base);
-                st[t][r] = p;
-                l += p;
+                    for (int r = 0; r < 4; r++) {
+                        const int key = k0 + 16 * t + 4 * grp + r;
+                        if (key > qrow || key >= T) st[t][qt][r] = -INFINITY;
+                    }
             }
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++)
-            pf[s2] = u32x4{pack2(st[2 * s2][0], st[2 * s2][1]), pack2(st[2 * s2][2], st[2 * s2][3]),
-                           pack2(st[2 * s2 + 1][0], st[2 * s2 + 1][1]), pack2(st[2 * s2 + 1][2], st[2 * s2 + 1][3])};
-        // O^T += V^T P^T; the k index 8 grp + e maps to key 32 s2 + 4 grp + e (e < 4) or
-        // 32 s2 + 16 + 4 grp + e - 4 (e >= 4), the same mapping on both operands
+            for (int t = 0; t < 4; t++)
+                mx = fmaxf(mx, fmaxf(fmaxf(st[t][qt][0], st[t][qt][1]), fmaxf(st[t][qt][2], st[t][qt][3])));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mn = fmaxf(m[qt], mx * scale_log2);
+            const float base = mn == -INFINITY ? 0.f : mn;
+            const float alpha = __builtin_amdgcn_exp2f(m[qt] - base);
+            m[qt] = mn;
+            l[qt] *= alpha;
+            // rescale only when some row's maximum moved (alpha == 1 is exact otherwise)
+            if (!__all(alpha == 1.f)) {
+#pragma unroll
+                for (int i = 0; i < DT; i++) o[qt][i] *= alpha;
+            }
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(st[t][qt][r], scale_log2, -base));
+                    st[t][qt][r] = p;
+                    l[qt] += p;
+                }
+            // P^T as the B operand of V^T P^T: key k index 8 grp + e is key 32 s2 + 4 grp + e
+            // (e < 4) or 32 s2 + 16 + 4 grp + e - 4 (e >= 4), the same order V^T is read in
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++)
+                pf[qt][s2] = u32x4{pack2(st[2 * s2][qt][0], st[2 * s2][qt][1]), pack2(st[2 * s2][qt][2], st[2 * s2][qt][3]),
+                                   pack2(st[2 * s2 + 1][qt][0], st[2 * s2 + 1][qt][1]),
+                                   pack2(st[2 * s2 + 1][qt][2], st[2 * s2 + 1][qt][3])};
+        }
+        FA_T(1);
+        // O^T += V^T P^T; each V^T fragment feeds both query tiles
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
-            const bf16* vr = vt + (16 * dt + col) * FaSmem<D>::VLD + 4 * grp;
+            const int d = 16 * dt + col;
+            const bf16* vr = vt + d * FaSmem<D>::VLD;
 #pragma unroll
             for (int s2 = 0; s2 < 2; s2++) {
-                const u32x2 a0 = *reinterpret_cast<const u32x2*>(vr + 32 * s2);
-                const u32x2 a1 = *reinterpret_cast<const u32x2*>(vr + 32 * s2 + 16);
-                o[dt] = mfma16(u32x4{a0[0], a0[1], a1[0], a1[1]}, pf[s2], o[dt]);
+                // keys 32 s2 + 4 grp .. + 3 and 32 s2 + 16 + 4 grp .. + 3 (pairs 16 s2 + 2 grp, + 8)
+                const u32x2 a0 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair(d, 16 * s2 + 2 * grp));
+                const u32x2 a1 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair(d, 16 * s2 + 8 + 2 * grp));
+                const u32x4 a = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                #pragma unroll
+                for (int qt = 0; qt < QT; qt++) o[qt][dt] = mfma16(a, pf[qt][s2], o[qt][dt]);
             }
         }
-    }
-
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    if (qrow >= T) return;
-    const float inv = 1.f / l;
-    bf16* dst = out + ((size_t)qrow * Hq + h) * D + 4 * grp;
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++) {
-        float a[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) a[r] = o[dt][r] * inv;
-        if (GATED) {
-            const u32x2 gp = *reinterpret_cast<const u32x2*>(gate + ((size_t)qrow * Hq + h) * D + 16 * dt + 4 * grp);
-            a[0] = round_bf16(a[0]) * round_bf16(sigmoid(lo_f32(gp[0])));
-            a[1] = round_bf16(a[1]) * round_bf16(sigmoid(hi_f32(gp[0])));
-            a[2] = round_bf16(a[2]) * round_bf16(sigmoid(lo_f32(gp[1])));
-            a[3] = round_bf16(a[3]) * round_bf16(sigmoid(hi_f32(gp[1])));
+        FA_T(2);
+        // next stage: tile + 1 from registers to LDS, then fetch tile + 2
+        if (tile + 1 < ntiles) {
+            bf16* nk = stage0 + ((tile + 1) & 1) * FaSmem<D>::STAGE;
+            store_tile<D>(regs, nk, nk + BN * FaSmem<D>::KLD);
+            if (tile + 2 < ntiles) load_tile<D>(regs, kh, vh, ldk, ldv, k0 + 2 * BN, T);
         }
-        *reinterpret_cast<u32x2*>(dst + 16 * dt) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
+        __syncthreads();
+        FA_T(3);
     }
-    if (lse != nullptr && grp == 0) lse[(size_t)h * T + qrow] = (m + log2f(l)) * 0.69314718055994531f;
+    FA_FLUSH();
+
+#pragma unroll
+    for (int qt = 0; qt < QT; qt++) {
+        float lt = l[qt];
+        lt += __shfl_xor(lt, 16, 64);
+        lt += __shfl_xor(lt, 32, 64);
+        const int qrow = q0 + 16 * qt + col;
+        if (qrow >= T) continue;
+        const float inv = 1.f / lt;
+        bf16* dst = out + ((size_t)qrow * Hq + h) * D + 4 * grp;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            float a[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) a[r] = o[qt][dt][r] * inv;
+            if (GATED) {
+                const u32x2 gp =
+                    *reinterpret_cast<const u32x2*>(gate + ((size_t)qrow * Hq + h) * D + 16 * dt + 4 * grp);
+                a[0] = round_bf16(a[0]) * round_bf16(sigmoid(lo_f32(gp[0])));
+                a[1] = round_bf16(a[1]) * round_bf16(sigmoid(hi_f32(gp[0])));
+                a[2] = round_bf16(a[2]) * round_bf16(sigmoid(lo_f32(gp[1])));
+                a[3] = round_bf16(a[3]) * round_bf16(sigmoid(hi_f32(gp[1])));
+            }
+            *reinterpret_cast<u32x2*>(dst + 16 * dt) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
+        }
+        if (lse != nullptr && grp == 0) lse[(size_t)h * T + qrow] = (m[qt] + log2f(lt)) * 0.69314718055994531f;
+    }
 }
 
-template <int D, bool GATED>
+template <int D, bool GATED, bool GQA4, int QT>
 int launch_flash(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse, int T,
                  int Hq, int Hk, float scale, int q_base, hipStream_t st) {
     static const hipError_t configured = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(flash_kernel<D, GATED>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        reinterpret_cast<const void*>(flash_kernel<D, GATED, GQA4, QT>), hipFuncAttributeMaxDynamicSharedMemorySize,
         FaSmem<D>::BYTES);
     if (configured != hipSuccess) return configured;
     constexpr float LOG2E = 1.4426950408889634f;
-    flash_kernel<D, GATED><<<dim3((T - q_base + BM - 1) / BM, Hq), FA_THREADS, FaSmem<D>::BYTES, st>>>(
+    const int nrows = (GQA4 ? 1 : 4) * 16 * QT;
+    const int blocks = (T - q_base + nrows - 1) / nrows * (GQA4 ? Hq / 4 : Hq);
+    flash_kernel<D, GATED, GQA4, QT><<<blocks, FA_THREADS, FaSmem<D>::BYTES, st>>>(
         static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
         static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, T, Hq, Hk, scale * LOG2E, q_base);
     return hipGetLastError();
+}
+
+template <int D, bool GATED>
+int launch_flash_any(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse,
+                     int T, int Hq, int Hk, float scale, int q_base, hipStream_t st) {
+    if ((Hq / Hk) % 4 == 0)
+        return launch_flash<D, GATED, true, 1>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
+    return launch_flash<D, GATED, false, 2>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -299,22 +397,28 @@ int attention_run(const void* q, const void* k, const void* v, int ldv, const vo
                   int T, int Hq, int Hk, int Dh, float scale, int q_base, void* stream) {
     if ((Dh != 128 && Dh != 256) || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || ldv % 8 != 0 || ldv < Hk * Dh || T < 0)
         return hipErrorInvalidValue;
-    if (q_base < 0 || q_base % BM || q_base > T) return hipErrorInvalidValue;
+    if (q_base < 0 || q_base % 64 || q_base > T) return hipErrorInvalidValue;
     if (T == q_base) return hipSuccess;
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || (gate && !aligned16(gate)))
         return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (Dh == 128)
-        return gate ? launch_flash<128, true>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st)
-                    : launch_flash<128, false>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
-    return gate ? launch_flash<256, true>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st)
-                : launch_flash<256, false>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
+        return gate ? launch_flash_any<128, true>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st)
+                    : launch_flash_any<128, false>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
+    return gate ? launch_flash_any<256, true>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st)
+                : launch_flash_any<256, false>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
 }
 
 }  // namespace
 }  // namespace q35
 
 using namespace q35;
+
+#ifdef Q35_PHASE_TIMING
+extern "C" int q35_debug_fa_ticks(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(q35_fa_ticks), sizeof(q35_fa_ticks));
+}
+#endif
 
 extern "C" int cs1_attn_prep(const void* qg, const void* kr, int ld, const void* qw, const void* kw, const void* cos,
                              const void* sin, void* q, void* gate, void* k, int T, int Hq, int Hk, int Dh, int half,

@@ -13,6 +13,8 @@ namespace q35 {
 using bf16 = uint16_t;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -26,8 +28,9 @@ __device__ __forceinline__ bf16 to_bf16(float x) {
     return __builtin_bit_cast(uint16_t, b);
 }
 __device__ __forceinline__ float round_bf16(float x) { return f32(to_bf16(x)); }
+// Two floats to a packed bf16 pair (round to nearest even), one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return (uint32_t)to_bf16(lo) | ((uint32_t)to_bf16(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
 }
 __device__ __forceinline__ float lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
@@ -79,6 +82,11 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 c)
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
 }
+
+// Wait until every outstanding vector memory load of this wave has completed (vmcnt(0),
+// lgkm/exp counters untouched). Placed before a loop so the compiler's wait analysis knows
+// one-time loads issued before it are done and does not re-wait on them every iteration.
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
 inline unsigned cdiv(size_t n, unsigned d) { return (unsigned)((n + d - 1) / d); }
 
