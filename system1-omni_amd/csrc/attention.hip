@@ -7,8 +7,10 @@
 //
 // flash_kernel: causal GQA attention, FlashAttention-2 structure, designed around the
 // wave64 MFMA v_mfma_f32_16x16x32_bf16:
-//   * a workgroup owns 64 queries of one head (four waves of 16 queries) and walks the
-//     keys up to its last query in tiles of 64, K row-major and V transposed in LDS;
+//   * a workgroup of eight waves owns 16 query rows of the four q-heads of a GQA group (or
+//     128 rows of one head); its key range is split by tile parity between two groups of
+//     four waves, halving the serial chain, and the partial softmax states are merged at
+//     the end; K row-major and V transposed (bank-swizzled) are double-buffered in LDS;
 //   * each wave computes S^T = K Q^T (keys on the MFMA M side, its 16 queries on N) so the
 //     accumulator layout (lane = query column, 4 consecutive keys per lane) is already the
 //     B-operand layout of O^T = V^T P^T: the probabilities never leave registers and every
@@ -82,49 +84,51 @@ __global__ void __launch_bounds__(256)
 
 // ---------------------------------------------------------------- flash attention
 
-constexpr int BN = 64;          // keys per tile
-constexpr int QW = 32;          // queries per wave (two 16-query MFMA column tiles)
-constexpr int FA_THREADS = 256; // four waves
+constexpr int FA_WAVES = 8;                  // two groups of four waves
+constexpr int FA_THREADS = 64 * FA_WAVES;
+constexpr int GROUP_THREADS = 256;
 
 template <int D>
-struct FaSmem {
-    static constexpr int KLD = D + 8;   // bf16 row stride of K [BN][D]
-    static constexpr int VLD = BN + 8;  // bf16 row stride of V^T [D][BN]
-    static constexpr int STAGE = BN * KLD + D * VLD;  // bf16 elements per stage
-    static constexpr int BYTES = 2 * STAGE * 2;        // two stages
+struct FaCfg {
+    static constexpr int BN = D == 128 ? 64 : 32;  // keys per tile
+    static constexpr int NSUB = BN / 16;           // 16-key score sub-tiles
+    static constexpr int KS2 = BN / 32;            // 32-key steps of P V
+    static constexpr int KLD = D + 8;              // bf16 row stride of K [BN][D]
+    static constexpr int VLD = BN + 8;             // bf16 row stride of V^T [D][BN]
+    static constexpr int STAGE = BN * KLD + D * VLD;           // bf16 elements per stage
+    static constexpr int BYTES = 4 * STAGE * 2;                // 2 groups x 2 stages
+    static constexpr int KP = BN * D / 8 / GROUP_THREADS;      // K packs per thread
+    static constexpr int VP = BN / 2 * D / 8 / GROUP_THREADS;  // V key pairs x 8 dims per thread
 };
 
 template <int D>
 struct TileRegs {
-    // this thread's share of one K tile and one V tile (16-byte packs)
-    static constexpr int KP = BN * D / 8 / FA_THREADS;        // K packs per thread
-    static constexpr int VP = BN / 2 * D / 8 / FA_THREADS;    // V key-pairs x 8 dims per thread
-    u32x4 k[KP];
-    u32x4 v[VP][2];
+    u32x4 k[FaCfg<D>::KP];
+    u32x4 v[FaCfg<D>::VP][2];
 };
 
-__device__ __forceinline__ u32x4 ldg16(const bf16* p) {
-    return *reinterpret_cast<const u32x4*>(p);
-}
+__device__ __forceinline__ u32x4 ldg16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// V^T column swizzle: key pair p of row d is stored at pair p ^ 2 ((d / 8) % 16). Groups of
-// four keys stay contiguous (fragment reads are unchanged in shape) while the transposing
-// stores of one wave, which cover rows 8c + 2e for c = 0..15, spread over all 64 banks.
-__device__ __forceinline__ int vt_pair(int d, int pair) { return pair ^ (((d >> 3) & 15) << 1); }
+// V^T column swizzle: key pair p of row d is stored at pair p ^ 2 ((d / 8) % 16) (within the
+// tile's pairs). Groups of four keys stay contiguous, and the transposing stores of one
+// wave (rows 8c + 2e, c = 0..15) spread over all 64 banks.
+template <int D>
+__device__ __forceinline__ int vt_pair(int d, int pair) {
+    return pair ^ ((((d >> 3) & 15) << 1) & (FaCfg<D>::BN / 2 - 1));
+}
 
 template <int D>
 __device__ __forceinline__ void load_tile(TileRegs<D>& r, const bf16* __restrict__ k, const bf16* __restrict__ v,
-                                          int ldk, int ldv, int k0, int T) {
-    const int tid = threadIdx.x;
+                                          int ldk, int ldv, int k0, int T, int tg) {
 #pragma unroll
-    for (int i = 0; i < TileRegs<D>::KP; i++) {
-        const int x = tid + i * FA_THREADS;
+    for (int i = 0; i < FaCfg<D>::KP; i++) {
+        const int x = tg + i * GROUP_THREADS;
         const int row = x / (D / 8), col = (x % (D / 8)) * 8, s = min(k0 + row, T - 1);
         r.k[i] = ldg16(k + (size_t)s * ldk + col);
     }
 #pragma unroll
-    for (int i = 0; i < TileRegs<D>::VP; i++) {
-        const int x = tid + i * FA_THREADS;
+    for (int i = 0; i < FaCfg<D>::VP; i++) {
+        const int x = tg + i * GROUP_THREADS;
         const int pair = x / (D / 8), col = (x % (D / 8)) * 8;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
@@ -135,77 +139,66 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& r, const bf16* __restrict
 }
 
 template <int D>
-__device__ __forceinline__ void store_tile(const TileRegs<D>& r, bf16* ks, bf16* vt) {
-    const int tid = threadIdx.x;
+__device__ __forceinline__ void store_tile(const TileRegs<D>& r, bf16* ks, int tg) {
+    bf16* vt = ks + FaCfg<D>::BN * FaCfg<D>::KLD;
 #pragma unroll
-    for (int i = 0; i < TileRegs<D>::KP; i++) {
-        const int x = tid + i * FA_THREADS;
+    for (int i = 0; i < FaCfg<D>::KP; i++) {
+        const int x = tg + i * GROUP_THREADS;
         const int row = x / (D / 8), col = (x % (D / 8)) * 8;
-        *reinterpret_cast<u32x4*>(ks + row * FaSmem<D>::KLD + col) = r.k[i];
+        *reinterpret_cast<u32x4*>(ks + row * FaCfg<D>::KLD + col) = r.k[i];
     }
 #pragma unroll
-    for (int i = 0; i < TileRegs<D>::VP; i++) {
-        const int x = tid + i * FA_THREADS;
+    for (int i = 0; i < FaCfg<D>::VP; i++) {
+        const int x = tg + i * GROUP_THREADS;
         const int pair = x / (D / 8), col = (x % (D / 8)) * 8;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             // dims col + 2e and col + 2e + 1 of keys 2 pair, 2 pair + 1
             const uint32_t a = r.v[i][0][e], b = r.v[i][1][e];
-            const uint32_t lo = (a & 0xffffu) | (b << 16);
-            const uint32_t hi = (a >> 16) | (b & 0xffff0000u);
+            const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);
+            const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);
             const int d0 = col + 2 * e, d1 = d0 + 1;
-            *reinterpret_cast<uint32_t*>(vt + d0 * FaSmem<D>::VLD + 2 * vt_pair(d0, pair)) = lo;
-            *reinterpret_cast<uint32_t*>(vt + d1 * FaSmem<D>::VLD + 2 * vt_pair(d1, pair)) = hi;
+            *reinterpret_cast<uint32_t*>(vt + d0 * FaCfg<D>::VLD + 2 * vt_pair<D>(d0, pair)) = lo;
+            *reinterpret_cast<uint32_t*>(vt + d1 * FaCfg<D>::VLD + 2 * vt_pair<D>(d1, pair)) = hi;
         }
     }
 }
 
 #ifdef Q35_PHASE_TIMING
-// Development aid: per-phase shader-clock ticks of the tile loop, summed over blocks.
 __device__ unsigned long long q35_fa_ticks[8];
-#define FA_T0() uint64_t fa_t0 = __builtin_amdgcn_s_memtime(), fa_acc[4] = {0, 0, 0, 0}
-#define FA_T(i)                                                 \
-    do {                                                        \
-        const uint64_t fa_t1 = __builtin_amdgcn_s_memtime();    \
-        fa_acc[i] += fa_t1 - fa_t0;                             \
-        fa_t0 = fa_t1;                                          \
-    } while (0)
-#define FA_FLUSH()                                                                                   \
-    do {                                                                                             \
-        if (threadIdx.x == 0) {                                                                      \
-            for (int fa_i = 0; fa_i < 4; fa_i++) atomicAdd(&q35_fa_ticks[fa_i], fa_acc[fa_i]);       \
-            atomicAdd(&q35_fa_ticks[4], (unsigned long long)ntiles);                                 \
-        }                                                                                            \
-    } while (0)
-#else
-#define FA_T0() (void)0
-#define FA_T(i) (void)0
-#define FA_FLUSH() (void)0
 #endif
 
-// Work split. GQA4 (Hq / Hk a multiple of 4): the four waves are four q-heads of one GQA
-// group on the same 32 query rows, so every K/V tile in LDS serves four heads. Otherwise
-// the four waves are four consecutive 32-row blocks of one head.
-template <int D, bool GATED, bool GQA4, int QT>
-__global__ void __launch_bounds__(FA_THREADS, D == 128 ? 2 : 1)
+// Work split of a block (eight waves): wave = 4 g + w. Group g processes the key tiles
+// t = g, g + 2, ... of the block's key range, so the block's serial chain is half its
+// length and the two groups interleave on every SIMD; their partial softmax states are
+// merged at the end. GQA4 (Hq / Hk a multiple of 4): w indexes four q-heads of one GQA group
+// on the same 16 query rows (every K/V tile in LDS serves four heads); otherwise w indexes
+// four consecutive 32-row (16 for Dh = 256) blocks of one head. Tile boundaries are fixed multiples of BN from
+// key 0 and the split is by tile parity, so a query row's arithmetic does not depend on how
+// rows are grouped into blocks (the windowed pass repeats the full pass bit for bit).
+template <int D, bool GATED, bool GQA4>
+__global__ void __launch_bounds__(FA_THREADS, 1)
     flash_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int ldv,
                  const bf16* __restrict__ gate, bf16* __restrict__ out, float* __restrict__ lse, int T, int Hq, int Hk,
                  float scale_log2, int q_base) {
+    using Cfg = FaCfg<D>;
+    constexpr int BN = Cfg::BN, QT = (GQA4 || D == 256) ? 1 : 2;
     extern __shared__ __align__(16) unsigned char smem[];
-    bf16* stage0 = reinterpret_cast<bf16*>(smem);
+    bf16* lds = reinterpret_cast<bf16*>(smem);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int grp_id = __builtin_amdgcn_readfirstlane(wave >> 2), w = wave & 3, tg = tid & (GROUP_THREADS - 1);
     const int col = lane & 15, grp = lane >> 4;
-    constexpr int QWW = 16 * QT;             // query rows per wave
-    const int nrows = GQA4 ? QWW : 4 * QWW;  // query rows per block
-    const int nblk = (T - q_base + nrows - 1) / nrows;
-    const int units = GQA4 ? Hq / 4 : Hq;  // head units per row block
+    constexpr int QWW = 16 * QT;                   // query rows per wave
+    constexpr int NROWS = GQA4 ? QWW : 4 * QWW;    // query rows per block
+    const int nblk = (T - q_base + NROWS - 1) / NROWS;
+    const int units = GQA4 ? Hq / 4 : Hq;
     const int b = blockIdx.x;
     const int rblk = nblk - 1 - b / units;  // longest blocks first
     const int unit = b % units;
-    const int h = GQA4 ? unit * 4 + wave : unit;
+    const int h = GQA4 ? unit * 4 + w : unit;
     const int hk = (GQA4 ? unit * 4 : unit) / (Hq / Hk);
-    const int blk_q0 = q_base + rblk * nrows;
-    const int q0 = blk_q0 + (GQA4 ? 0 : wave * QWW);  // this wave's first query
+    const int blk_q0 = q_base + rblk * NROWS;
+    const int q0 = blk_q0 + (GQA4 ? 0 : w * QWW);  // this wave's first query
     const bf16* kh = k + (size_t)hk * D;
     const bf16* vh = v + (size_t)hk * D;
     const int ldk = Hk * D;
@@ -217,131 +210,156 @@ __global__ void __launch_bounds__(FA_THREADS, D == 128 ? 2 : 1)
     for (int qt = 0; qt < QT; qt++) {
         const bf16* qr = q + ((size_t)min(q0 + 16 * qt + col, T - 1) * Hq + h) * D + 8 * grp;
 #pragma unroll
-        for (int s = 0; s < KS; s++) {
-            const Pack8 p = *reinterpret_cast<const Pack8*>(qr + 32 * s);
-            qf[qt][s] = u32x4{p.w[0], p.w[1], p.w[2], p.w[3]};
-        }
+        for (int s = 0; s < KS; s++) qf[qt][s] = ldg16(qr + 32 * s);
     }
 
     constexpr int DT = D / 16;
     f32x4 o[QT][DT];
-#pragma unroll
-    for (int qt = 0; qt < QT; qt++)
-#pragma unroll
-        for (int i = 0; i < DT; i++) o[qt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m[QT], l[QT];
 #pragma unroll
-    for (int qt = 0; qt < QT; qt++) m[qt] = -INFINITY, l[qt] = 0.f;
+    for (int qt = 0; qt < QT; qt++) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.f;
+#pragma unroll
+        for (int i = 0; i < DT; i++) o[qt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
-    const int kv_end = min(T, blk_q0 + nrows);
+    const int kv_end = min(T, blk_q0 + NROWS);
     const int ntiles = (kv_end + BN - 1) / BN;
+    const int nt0 = (ntiles + 1) / 2;                // group 0's tiles (>= group 1's)
+    const int ntg = grp_id == 0 ? nt0 : ntiles / 2;  // this group's tiles
+    bf16* gstage = lds + grp_id * 2 * Cfg::STAGE;
+
     TileRegs<D> regs;
-    load_tile<D>(regs, kh, vh, ldk, ldv, 0, T);
-    wait_vm_all();  // Q fragments and tile 0 are in registers
-    store_tile<D>(regs, stage0, stage0 + BN * FaSmem<D>::KLD);
-    if (ntiles > 1) load_tile<D>(regs, kh, vh, ldk, ldv, BN, T);
+    if (ntg > 0) {
+        load_tile<D>(regs, kh, vh, ldk, ldv, grp_id * BN, T, tg);
+        wait_vm_all();  // Q fragments and the first tile are in registers
+        store_tile<D>(regs, gstage, tg);
+        if (ntg > 1) load_tile<D>(regs, kh, vh, ldk, ldv, (2 + grp_id) * BN, T, tg);
+    }
+    wait_vm_all();
     __syncthreads();
-    FA_T0();
-    for (int tile = 0; tile < ntiles; tile++) {
-        const int k0 = tile * BN;
-        const bf16* ks = stage0 + (tile & 1) * FaSmem<D>::STAGE;
-        const bf16* vt = ks + BN * FaSmem<D>::KLD;
-        // S^T = K Q^T: 4 sub-tiles of 16 keys x 2 query tiles; each K fragment feeds both
-        f32x4 st[4][QT];
+    for (int it = 0; it < nt0; it++) {
+        const int tile = 2 * it + grp_id;
+        const bool live = it < ntg;  // wave-uniform
+        const bf16* ks = gstage + (it & 1) * Cfg::STAGE;
+        const bf16* vt = ks + BN * Cfg::KLD;
+        if (live) {
+            const int k0 = tile * BN;
+            // S^T = K Q^T: NSUB sub-tiles of 16 keys x QT query tiles
+            f32x4 st[Cfg::NSUB][QT];
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            #pragma unroll
-            for (int qt = 0; qt < QT; qt++) st[t][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            const bf16* kr = ks + (16 * t + col) * FaSmem<D>::KLD + 8 * grp;
+            for (int t = 0; t < Cfg::NSUB; t++) {
 #pragma unroll
-            for (int s = 0; s < KS; s++) {
-                const Pack8 p = *reinterpret_cast<const Pack8*>(kr + 32 * s);
-                const u32x4 a = u32x4{p.w[0], p.w[1], p.w[2], p.w[3]};
-                #pragma unroll
-                for (int qt = 0; qt < QT; qt++) st[t][qt] = mfma16(a, qf[qt][s], st[t][qt]);
+                for (int qt = 0; qt < QT; qt++) st[t][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const bf16* kr = ks + (16 * t + col) * Cfg::KLD + 8 * grp;
+#pragma unroll
+                for (int s = 0; s < KS; s++) {
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(kr + 32 * s);
+#pragma unroll
+                    for (int qt = 0; qt < QT; qt++) st[t][qt] = mfma16(a, qf[qt][s], st[t][qt]);
+                }
             }
-        }
-        FA_T(0);
-        u32x4 pf[QT][2];
-        // Only the tiles that reach the diagonal of this wave's rows or past T need the mask
-        // (wave-uniform test); elsewhere every key is visible to every row.
-        const bool masked = k0 + BN - 1 > q0 || k0 + BN > T;
+            u32x4 pf[QT][Cfg::KS2];
+            // only tiles reaching the diagonal of this wave's rows or past T need the mask
+            const bool masked = k0 + BN - 1 > q0 || k0 + BN > T;
 #pragma unroll
-        for (int qt = 0; qt < QT; qt++) {
-            const int qrow = q0 + 16 * qt + col;
-            // running max of the raw scores (scale > 0), over the 4 lanes {q, q+16, q+32, q+48}
-            float mx = -INFINITY;
-            if (masked) {
+            for (int qt = 0; qt < QT; qt++) {
+                const int qrow = q0 + 16 * qt + col;
+                if (masked) {
 #pragma unroll
-                for (int t = 0; t < 4; t++)
+                    for (int t = 0; t < Cfg::NSUB; t++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const int key = k0 + 16 * t + 4 * grp + r;
+                            if (key > qrow || key >= T) st[t][qt][r] = -INFINITY;
+                        }
+                }
+                // running max of the raw scores (scale > 0) over the lanes {q, q+16, q+32, q+48}
+                float mx = -INFINITY;
+#pragma unroll
+                for (int t = 0; t < Cfg::NSUB; t++)
+                    mx = fmaxf(mx, fmaxf(fmaxf(st[t][qt][0], st[t][qt][1]), fmaxf(st[t][qt][2], st[t][qt][3])));
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float mn = fmaxf(m[qt], mx * scale_log2);
+                const float base = mn == -INFINITY ? 0.f : mn;
+                const float alpha = __builtin_amdgcn_exp2f(m[qt] - base);
+                m[qt] = mn;
+                l[qt] *= alpha;
+                // rescale only when some row's maximum moved (alpha == 1 is exact otherwise)
+                if (!__all(alpha == 1.f)) {
+#pragma unroll
+                    for (int i = 0; i < DT; i++) o[qt][i] *= alpha;
+                }
+#pragma unroll
+                for (int t = 0; t < Cfg::NSUB; t++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        const int key = k0 + 16 * t + 4 * grp + r;
-                        if (key > qrow || key >= T) st[t][qt][r] = -INFINITY;
+                        const float p = __builtin_amdgcn_exp2f(fmaf(st[t][qt][r], scale_log2, -base));
+                        st[t][qt][r] = p;
+                        l[qt] += p;
                     }
+                // P^T as the B operand of V^T P^T: k index 8 grp + e is key 32 s2 + 4 grp + e
+                // (e < 4) or 32 s2 + 16 + 4 grp + e - 4 (e >= 4), the order V^T is read in
+#pragma unroll
+                for (int s2 = 0; s2 < Cfg::KS2; s2++)
+                    pf[qt][s2] = u32x4{pack2(st[2 * s2][qt][0], st[2 * s2][qt][1]), pack2(st[2 * s2][qt][2], st[2 * s2][qt][3]),
+                                       pack2(st[2 * s2 + 1][qt][0], st[2 * s2 + 1][qt][1]),
+                                       pack2(st[2 * s2 + 1][qt][2], st[2 * s2 + 1][qt][3])};
             }
+            // O^T += V^T P^T; each V^T fragment feeds every query tile
 #pragma unroll
-            for (int t = 0; t < 4; t++)
-                mx = fmaxf(mx, fmaxf(fmaxf(st[t][qt][0], st[t][qt][1]), fmaxf(st[t][qt][2], st[t][qt][3])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mn = fmaxf(m[qt], mx * scale_log2);
-            const float base = mn == -INFINITY ? 0.f : mn;
-            const float alpha = __builtin_amdgcn_exp2f(m[qt] - base);
-            m[qt] = mn;
-            l[qt] *= alpha;
-            // rescale only when some row's maximum moved (alpha == 1 is exact otherwise)
-            if (!__all(alpha == 1.f)) {
+            for (int dt = 0; dt < DT; dt++) {
+                const int d = 16 * dt + col;
+                const bf16* vr = vt + d * Cfg::VLD;
 #pragma unroll
-                for (int i = 0; i < DT; i++) o[qt][i] *= alpha;
-            }
+                for (int s2 = 0; s2 < Cfg::KS2; s2++) {
+                    // keys 32 s2 + 4 grp .. + 3 and 32 s2 + 16 + 4 grp .. + 3
+                    const u32x2 a0 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair<D>(d, 16 * s2 + 2 * grp));
+                    const u32x2 a1 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair<D>(d, 16 * s2 + 8 + 2 * grp));
+                    const u32x4 a = u32x4{a0[0], a0[1], a1[0], a1[1]};
 #pragma unroll
-            for (int t = 0; t < 4; t++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(st[t][qt][r], scale_log2, -base));
-                    st[t][qt][r] = p;
-                    l[qt] += p;
+                    for (int qt = 0; qt < QT; qt++) o[qt][dt] = mfma16(a, pf[qt][s2], o[qt][dt]);
                 }
-            // P^T as the B operand of V^T P^T: key k index 8 grp + e is key 32 s2 + 4 grp + e
-            // (e < 4) or 32 s2 + 16 + 4 grp + e - 4 (e >= 4), the same order V^T is read in
-#pragma unroll
-            for (int s2 = 0; s2 < 2; s2++)
-                pf[qt][s2] = u32x4{pack2(st[2 * s2][qt][0], st[2 * s2][qt][1]), pack2(st[2 * s2][qt][2], st[2 * s2][qt][3]),
-                                   pack2(st[2 * s2 + 1][qt][0], st[2 * s2 + 1][qt][1]),
-                                   pack2(st[2 * s2 + 1][qt][2], st[2 * s2 + 1][qt][3])};
-        }
-        FA_T(1);
-        // O^T += V^T P^T; each V^T fragment feeds both query tiles
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            const int d = 16 * dt + col;
-            const bf16* vr = vt + d * FaSmem<D>::VLD;
-#pragma unroll
-            for (int s2 = 0; s2 < 2; s2++) {
-                // keys 32 s2 + 4 grp .. + 3 and 32 s2 + 16 + 4 grp .. + 3 (pairs 16 s2 + 2 grp, + 8)
-                const u32x2 a0 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair(d, 16 * s2 + 2 * grp));
-                const u32x2 a1 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair(d, 16 * s2 + 8 + 2 * grp));
-                const u32x4 a = u32x4{a0[0], a0[1], a1[0], a1[1]};
-                #pragma unroll
-                for (int qt = 0; qt < QT; qt++) o[qt][dt] = mfma16(a, pf[qt][s2], o[qt][dt]);
             }
         }
-        FA_T(2);
-        // next stage: tile + 1 from registers to LDS, then fetch tile + 2
-        if (tile + 1 < ntiles) {
-            bf16* nk = stage0 + ((tile + 1) & 1) * FaSmem<D>::STAGE;
-            store_tile<D>(regs, nk, nk + BN * FaSmem<D>::KLD);
-            if (tile + 2 < ntiles) load_tile<D>(regs, kh, vh, ldk, ldv, k0 + 2 * BN, T);
+        // next tile of each group: registers to the other stage, then fetch the one after
+        if (it + 1 < nt0) {
+            __syncthreads();  // both groups are done with their other stage
+            if (it + 1 < ntg) {
+                store_tile<D>(regs, gstage + ((it + 1) & 1) * Cfg::STAGE, tg);
+                if (it + 2 < ntg) load_tile<D>(regs, kh, vh, ldk, ldv, (2 * (it + 2) + grp_id) * BN, T, tg);
+            }
+            __syncthreads();
         }
-        __syncthreads();
-        FA_T(3);
     }
-    FA_FLUSH();
 
+    // merge the two groups' partial states through LDS: group 1 publishes, group 0 finishes
+    __syncthreads();
+    float* part = reinterpret_cast<float*>(smem) + (size_t)w * 64 * (QT * (DT * 4 + 2));
+    if (grp_id == 1) {
+#pragma unroll
+        for (int qt = 0; qt < QT; qt++) {
+            float* pp = part + qt * (DT * 4 + 2) * 64;
+#pragma unroll
+            for (int i = 0; i < DT; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) pp[(i * 4 + r) * 64 + lane] = o[qt][i][r];
+            pp[(DT * 4) * 64 + lane] = m[qt];
+            pp[(DT * 4 + 1) * 64 + lane] = l[qt];
+        }
+    }
+    __syncthreads();
+    if (grp_id == 1) return;
 #pragma unroll
     for (int qt = 0; qt < QT; qt++) {
-        float lt = l[qt];
+        const float* pp = part + qt * (DT * 4 + 2) * 64;
+        const float m1 = pp[(DT * 4) * 64 + lane], l1 = pp[(DT * 4 + 1) * 64 + lane];
+        const float mm = fmaxf(m[qt], m1);
+        const float base = mm == -INFINITY ? 0.f : mm;
+        const float a0 = __builtin_amdgcn_exp2f(m[qt] - base), a1 = __builtin_amdgcn_exp2f(m1 - base);
+        float lt = l[qt] * a0 + l1 * a1;
         lt += __shfl_xor(lt, 16, 64);
         lt += __shfl_xor(lt, 32, 64);
         const int qrow = q0 + 16 * qt + col;
@@ -352,7 +370,7 @@ __global__ void __launch_bounds__(FA_THREADS, D == 128 ? 2 : 1)
         for (int dt = 0; dt < DT; dt++) {
             float a[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) a[r] = o[qt][dt][r] * inv;
+            for (int r = 0; r < 4; r++) a[r] = (o[qt][dt][r] * a0 + pp[(dt * 4 + r) * 64 + lane] * a1) * inv;
             if (GATED) {
                 const u32x2 gp =
                     *reinterpret_cast<const u32x2*>(gate + ((size_t)qrow * Hq + h) * D + 16 * dt + 4 * grp);
@@ -363,21 +381,21 @@ __global__ void __launch_bounds__(FA_THREADS, D == 128 ? 2 : 1)
             }
             *reinterpret_cast<u32x2*>(dst + 16 * dt) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
         }
-        if (lse != nullptr && grp == 0) lse[(size_t)h * T + qrow] = (m[qt] + log2f(lt)) * 0.69314718055994531f;
+        if (lse != nullptr && grp == 0) lse[(size_t)h * T + qrow] = (mm + log2f(lt)) * 0.69314718055994531f;
     }
 }
 
-template <int D, bool GATED, bool GQA4, int QT>
+template <int D, bool GATED, bool GQA4>
 int launch_flash(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse, int T,
                  int Hq, int Hk, float scale, int q_base, hipStream_t st) {
     static const hipError_t configured = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(flash_kernel<D, GATED, GQA4, QT>), hipFuncAttributeMaxDynamicSharedMemorySize,
-        FaSmem<D>::BYTES);
+        reinterpret_cast<const void*>(flash_kernel<D, GATED, GQA4>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        FaCfg<D>::BYTES);
     if (configured != hipSuccess) return configured;
     constexpr float LOG2E = 1.4426950408889634f;
-    const int nrows = (GQA4 ? 1 : 4) * 16 * QT;
+    const int nrows = GQA4 ? 16 : (D == 256 ? 64 : 128);
     const int blocks = (T - q_base + nrows - 1) / nrows * (GQA4 ? Hq / 4 : Hq);
-    flash_kernel<D, GATED, GQA4, QT><<<blocks, FA_THREADS, FaSmem<D>::BYTES, st>>>(
+    flash_kernel<D, GATED, GQA4><<<blocks, FA_THREADS, FaCfg<D>::BYTES, st>>>(
         static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
         static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, T, Hq, Hk, scale * LOG2E, q_base);
     return hipGetLastError();
@@ -387,8 +405,8 @@ template <int D, bool GATED>
 int launch_flash_any(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse,
                      int T, int Hq, int Hk, float scale, int q_base, hipStream_t st) {
     if ((Hq / Hk) % 4 == 0)
-        return launch_flash<D, GATED, true, 1>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
-    return launch_flash<D, GATED, false, 2>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
+        return launch_flash<D, GATED, true>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
+    return launch_flash<D, GATED, false>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
