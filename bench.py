@@ -75,22 +75,36 @@ def unit_rows_bf16(rng, rows, d):
 
 
 def timed(stream, ev, steps, warmup, launches):
-    """Run `launches` (list of (name, fn)) per step; return wall ms/step and per-name avg ms."""
+    """Run `launches` (list of (name, fn)) per step.
+
+    Returns the wall ms per step (host clock, stream synchronised on both sides of the K
+    steps) and each launch's average GPU ms. The per-launch figure is one HIP event pair on
+    the kernels' own stream around K back-to-back launches of that entry point alone (for a
+    one-launch step this is the step region itself), so no event marker sits between two
+    dispatches being timed."""
     for _ in range(warmup):
         for _, fn in launches:
             fn()
     stream.sync()
-    marks = [[ev.new() for _ in range(len(launches) + 1)] for _ in range(steps)]
+    e0, e1 = ev.new(), ev.new()
     t0 = time.perf_counter()
-    for s in range(steps):
-        ev.record(marks[s][0], stream)
-        for i, (_, fn) in enumerate(launches):
+    ev.record(e0, stream)
+    for _ in range(steps):
+        for _, fn in launches:
             fn()
-            ev.record(marks[s][i + 1], stream)
+    ev.record(e1, stream)
     stream.sync()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    per = {name: sum(ev.ms(marks[s][i], marks[s][i + 1]) for s in range(steps)) / steps
-           for i, (name, _) in enumerate(launches)}
+    if len(launches) == 1:
+        return wall_ms, {launches[0][0]: ev.ms(e0, e1) / steps}
+    per = {}
+    for name, fn in launches:
+        a, b = ev.new(), ev.new()
+        ev.record(a, stream)
+        for _ in range(steps):
+            fn()
+        ev.record(b, stream)
+        per[name] = ev.ms(a, b) / steps
     return wall_ms, per
 
 
@@ -186,7 +200,7 @@ def cpu_baseline_attention():
     while True:
         O.attention_emul(q, k, v, Hk * Dh, gate, T, Hq, Hk, Dh, Dh ** -0.5, want_lse=True)
         n += 1
-        if time.perf_counter() - t0 > 10 or n >= 20:
+        if time.perf_counter() - t0 > 10:
             break
     dt = time.perf_counter() - t0
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
@@ -195,13 +209,116 @@ def cpu_baseline_attention():
                       f"emulation of the reference flash kernel, OpenMP over query rows"}
 
 
+PROBE_COPY_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_bench_probe.txt")
+
+
+def probe(api, st):
+    """A short fixed sequence for the rocprofv3 counter passes: each workload's kernels a few
+    times, then a plain device-to-device copy of PROBE_COPY_BYTES that calibrates the
+    FETCH_SIZE / WRITE_SIZE counters (it reads and writes exactly that many bytes)."""
+    ev = Events()
+    bench_attention(api, st, ev, 3, 0)
+    bench_gdn(api, st, ev, 3, 0, 8192, 32, 16, True, 0.01, 2, "cfg2")
+    bench_gdn(api, st, ev, 3, 0, 512, 16, 16, False, 0.0, 0, "cfg0")
+    src, dst = hip.DeviceBuffer(PROBE_COPY_BYTES), hip.DeviceBuffer(PROBE_COPY_BYTES)
+    for _ in range(3):
+        hip.check(api.cs1_copy_dd(dst.at(0), src.at(0), PROBE_COPY_BYTES, st.handle), "copy")
+    st.sync()
+
+
+def _kernel_base(name):
+    """Demangled kernel name without its trailing argument list and leading `void `."""
+    name = name.strip()
+    if name.endswith(")"):
+        depth = 0
+        for i in range(len(name) - 1, -1, -1):
+            depth += {")": 1, "(": -1}.get(name[i], 0)
+            if depth == 0:
+                name = name[:i]
+                break
+    return name[5:] if name.startswith("void ") else name
+
+
+def summarize_pmc(dirs):
+    """Per-kernel averages of FETCH_SIZE / WRITE_SIZE (KiB per dispatch) from rocprofv3
+    counter CSVs of `bench.py --probe`, scaled by the calibration copy: bytes = KiB * scale,
+    scale = copy bytes / the copy's own counter reading."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    vals = defaultdict(lambda: defaultdict(list))
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                name = r["Kernel_Name"]
+                key = ("copy" if "copyBuffer" in name else _kernel_base(name)) + f" grid={r['Grid_Size']}"
+                vals[key][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    avg = {k: {c: sum(v) / len(v) for c, v in cs.items()} for k, cs in vals.items()}
+    copy = [v for k, v in avg.items() if k.startswith("copy")]
+    lines = []
+    scale = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        got = [v[c] for v in copy if c in v]
+        if got:
+            scale[c] = PROBE_COPY_BYTES / max(got)
+            lines.append(f"calibration {c}: copy of {PROBE_COPY_BYTES} B reads {max(got):.0f} KiB -> "
+                         f"{scale[c]:.2f} B per counted KiB")
+    for k, v in sorted(avg.items()):
+        if k.startswith("copy"):
+            continue
+        f = v.get("FETCH_SIZE", 0.0) * scale.get("FETCH_SIZE", 1024.0)
+        w = v.get("WRITE_SIZE", 0.0) * scale.get("WRITE_SIZE", 1024.0)
+        lines.append(f"traffic {k} fetch_kib={v.get('FETCH_SIZE', float('nan')):.0f} "
+                     f"write_kib={v.get('WRITE_SIZE', float('nan')):.0f} bytes={f + w:.0f}")
+    return "\n".join(lines)
+
+
+def summarize_trace(dirs):
+    """Per-kernel dispatch count and average / min / max duration (us) by grid size from
+    rocprofv3 --kernel-trace CSVs."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    dur = defaultdict(list)
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                key = _kernel_base(r["Kernel_Name"]) + f" grid={r['Grid_Size_X']}x{r['Grid_Size_Y']}"
+                dur[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return "\n".join(f"kernel {k} n={len(v)} avg_us={sum(v) / len(v):.2f} min_us={min(v):.2f} max_us={max(v):.2f}"
+                     for k, v in sorted(dur.items()))
+
+
+def traffic_bytes(kernel_prefix):
+    """HBM bytes per launch of a kernel from the committed counter summary, or None."""
+    try:
+        for ln in open(TRAFFIC_FILE):
+            if ln.startswith("traffic " + kernel_prefix):
+                return float(ln.rsplit("bytes=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--probe", action="store_true", help="short kernel sequence for rocprofv3 counter passes")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR", help="summarize rocprofv3 --pmc output of --probe")
+    ap.add_argument("--summarize-trace", nargs="+", metavar="DIR", help="summarize rocprofv3 --kernel-trace output")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        print(summarize_pmc(args.summarize_pmc))
+        return
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the prefill is sharded by heads in "
               "design only); run with --gpus 1", file=sys.stderr)
@@ -209,6 +326,9 @@ def main():
     api = hip.load()
     hip.set_device(0)
     st = hip.Stream()
+    if args.probe:
+        probe(api, st)
+        return
     ev = Events()
     attn = bench_attention(api, st, ev, args.steps, args.warmup)
     g2 = bench_gdn(api, st, ev, args.steps, args.warmup, 8192, 32, 16, True, 0.01, 2,
@@ -222,7 +342,8 @@ def main():
         "warmup": args.warmup, "ms_per_step": attn["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs of the BASELINE shapes)",
         "config": {"workload": attn["workload"], "global_batch": 1, "seq_len": 2048, "parallelism": "none"},
-        "roofline": {k: attn["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac")} | {"traffic": None},
+        "roofline": {k: attn["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac")} |
+                    {"traffic": traffic_bytes("q35::(anonymous namespace)::flash_kernel<128, true, true>")},
         "cpu_baseline": cpu,
         "layers": {"attention_cfg1": attn, "gdn_cfg2": g2, "gdn_cfg0": g0},
         "decision_prefill_ms_4k": None,
