@@ -188,6 +188,49 @@ def bench_gdn(api, st, ev, steps, warmup, T, H, HK, with_conv, s0_std, seed, lab
     return res
 
 
+def bench_hbm_ops(api, st, ev, steps, warmup):
+    """The HBM-bound operations around the two layers, each against the HBM peak with its
+    algorithmic bytes (read once + written once): the GDN gates and gated RMSNorm at config 2
+    (T=8192, 32 v heads, D=128) and the attention q/k prep at the config-3 attention shape
+    (T=4096, 16 q / 4 kv heads, Dh=256, rotary half 32)."""
+    rng = np.random.default_rng(3)
+    res = {}
+
+    def entry(name, workload, nbytes, fn):
+        wall, per = timed(st, ev, steps, warmup, [(name, fn)])
+        gbs = nbytes / (per[name] * 1e-3) / 1e9
+        res[name] = {"workload": workload, "kernel_ms": per[name], "bound": "hbm", "achieved": gbs,
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "algorithmic_bytes": nbytes}
+
+    T, H, D = 8192, 32, 128
+    ab = hip.to_device(bf16(rng, 2 * T * 2 * H), st)  # rows [b (H) | a (H)], ld = 2 H
+    alog = hip.to_device(bf16(rng, H, 0.5), st)
+    dtb = hip.to_device(bf16(rng, H), st)
+    beta, g = hip.DeviceBuffer(T * H * 2), hip.DeviceBuffer(T * H * 4)
+    entry("gdn_gates", "cfg2 gates T=8192 H=32", T * H * 10,
+          lambda: hip.check(api.cs1_gdn_gates(ab.at(0), ab.at(H * 2), 2 * H, alog.at(0), dtb.at(0), beta.at(0),
+                                              g.at(0), T, H, st.handle), "gates"))
+    x = hip.to_device(bf16(rng, T * H * D), st)
+    z = hip.to_device(bf16(rng, T * H * D), st)
+    w = hip.to_device(bf16(rng, D), st)
+    out = hip.DeviceBuffer(T * H * D * 2)
+    entry("gated_rms_norm", "cfg2 gated RMSNorm T=8192 H=32 D=128", 3 * T * H * D * 2,
+          lambda: hip.check(api.cs1_gated_rms_norm(x.at(0), z.at(0), H * D, w.at(0), out.at(0), T, H, D, 1e-6,
+                                                   st.handle), "gated norm"))
+    T, Hq, Hk, Dh, half = 4096, 16, 4, 256, 32
+    ld = Hq * 2 * Dh + 2 * Hk * Dh
+    row = hip.to_device(bf16(rng, T * ld), st)
+    qw, kw = hip.to_device(bf16(rng, Dh, 0.1), st), hip.to_device(bf16(rng, Dh, 0.1), st)
+    cs, sn = hip.to_device(bf16(rng, T * half), st), hip.to_device(bf16(rng, T * half), st)
+    q, gate, k = hip.DeviceBuffer(T * Hq * Dh * 2), hip.DeviceBuffer(T * Hq * Dh * 2), hip.DeviceBuffer(T * Hk * Dh * 2)
+    nbytes = T * (Hq * 2 * Dh + Hk * Dh) * 2 + 2 * T * half * 2 + T * (2 * Hq + Hk) * Dh * 2
+    entry("attn_prep", "cfg3 attention prep T=4096 Hq=16 Hk=4 Dh=256 half=32", nbytes,
+          lambda: hip.check(api.cs1_attn_prep(row.at(0), row.at(Hq * 2 * Dh * 2), ld, qw.at(0), kw.at(0), cs.at(0),
+                                              sn.at(0), q.at(0), gate.at(0), k.at(0), T, Hq, Hk, Dh, half, 1e-6,
+                                              st.handle), "attn prep"))
+    return res
+
+
 def cpu_baseline_attention():
     """The oracle's emulation of the reference flash kernel (C, OpenMP) on this host, over
     the full config-1 layer, repeated until about 10 s of work."""
@@ -221,6 +264,7 @@ def probe(api, st):
     bench_attention(api, st, ev, 3, 0)
     bench_gdn(api, st, ev, 3, 0, 8192, 32, 16, True, 0.01, 2, "cfg2")
     bench_gdn(api, st, ev, 3, 0, 512, 16, 16, False, 0.0, 0, "cfg0")
+    bench_hbm_ops(api, st, ev, 3, 0)
     src, dst = hip.DeviceBuffer(PROBE_COPY_BYTES), hip.DeviceBuffer(PROBE_COPY_BYTES)
     for _ in range(3):
         hip.check(api.cs1_copy_dd(dst.at(0), src.at(0), PROBE_COPY_BYTES, st.handle), "copy")
@@ -335,6 +379,7 @@ def main():
                    "cfg2 conv1d(k=4)+SiLU then GDN chunked prefill T=8192 HK=16 H=32 D=128, S0~N(0,0.01)")
     g0 = bench_gdn(api, st, ev, args.steps, args.warmup, 512, 16, 16, False, 0.0, 0,
                    "cfg0 GDN chunked prefill T=512 H=HK=16 D=128, S0=0")
+    hbm = bench_hbm_ops(api, st, ev, args.steps, args.warmup)
     cpu = None if args.no_cpu else cpu_baseline_attention()
     line = {
         "metric": "prefill tokens/s per layer type + ms per 4k-token hybrid decision prefill",
@@ -346,6 +391,7 @@ def main():
                     {"traffic": traffic_bytes("q35::(anonymous namespace)::flash_kernel<128, true, true>")},
         "cpu_baseline": cpu,
         "layers": {"attention_cfg1": attn, "gdn_cfg2": g2, "gdn_cfg0": g0},
+        "hbm_ops": hbm,
         "decision_prefill_ms_4k": None,
     }
     print(json.dumps(line), flush=True)
