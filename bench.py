@@ -231,6 +231,47 @@ def bench_hbm_ops(api, st, ev, steps, warmup):
     return res
 
 
+def bench_decision_prefill(steps, warmup, T=4096):
+    """one 4096-token decision prefill of the random-init 4B-class hybrid
+    decoder (32 layers, 3:1 GDN:attention, hidden 2560, SwiGLU 9728, 16/4 x 256 attention,
+    GDN 16 qk / 32 v heads) through the native runner, then the 8-label head on the last
+    hidden state. A step is one complete q35m_decide call: id upload, embedding, the layer
+    stack (a captured hipGraph after the first call at this length), the last-row download
+    and the host head; wall-clock ms."""
+    from qwen3_5_native import model as QM
+
+    cfg = QM.CFG3_4B
+    m = QM.Model(cfg, seed=0, max_tokens=T)
+    try:
+        m.set_graph(True)
+        rng = np.random.default_rng(4)
+        ids = rng.integers(0, cfg.vocab, T).astype(np.int32)
+        labels = (np.arange(8) * 997 + 151).astype(np.int32)
+        for _ in range(max(warmup, 2)):
+            logits = m.decide(ids, labels)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            logits = m.decide(ids, labels)
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+    finally:
+        m.close()
+    kd, vd = cfg.lin_k_heads * cfg.lin_k_dim, cfg.lin_v_heads * cfg.lin_v_dim
+    n_attn = sum(cfg.is_full(i) for i in range(cfg.layers))
+    n_gdn = cfg.layers - n_attn
+    gdn_w = 2 * kd + 2 * vd + 2 * cfg.lin_v_heads
+    attn_w = 2 * cfg.heads * cfg.head_dim + 2 * cfg.kv_heads * cfg.head_dim
+    per_token_gemm = (n_gdn * (gdn_w * cfg.hidden + cfg.hidden * vd) +
+                      n_attn * (attn_w * cfg.hidden + cfg.hidden * cfg.heads * cfg.head_dim) +
+                      cfg.layers * 3 * cfg.hidden * cfg.intermediate)
+    flop = (2.0 * T * per_token_gemm + n_attn * 2.0 * T * T * cfg.head_dim * cfg.heads +
+            n_gdn * 180224.0 * T * cfg.lin_v_heads)
+    return ms, {"workload": "cfg3 random-init 4B-class hybrid decoder (32 layers, 24 GDN + 8 gated attention), "
+                            "T=4096 decision prefill + 8-label head, hipGraph replay",
+                "ms_per_decision": ms, "argmax": int(np.argmax(logits)),
+                "algorithmic_flop": flop, "achieved_TFLOPs": flop / (ms * 1e-3) / 1e12,
+                "frac_of_bf16_peak": flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+
+
 def cpu_baseline_attention():
     """The oracle's emulation of the reference flash kernel (C, OpenMP) on this host, over
     the full config-1 layer, repeated until about 10 s of work."""
@@ -354,6 +395,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--probe", action="store_true", help="short kernel sequence for rocprofv3 counter passes")
+    ap.add_argument("--no-model", action="store_true", help="skip the config-3 decision prefill")
     ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR", help="summarize rocprofv3 --pmc output of --probe")
     ap.add_argument("--summarize-trace", nargs="+", metavar="DIR", help="summarize rocprofv3 --kernel-trace output")
     args = ap.parse_args()
@@ -380,6 +422,7 @@ def main():
     g0 = bench_gdn(api, st, ev, args.steps, args.warmup, 512, 16, 16, False, 0.0, 0,
                    "cfg0 GDN chunked prefill T=512 H=HK=16 D=128, S0=0")
     hbm = bench_hbm_ops(api, st, ev, args.steps, args.warmup)
+    dec_ms, dec = (None, None) if args.no_model else bench_decision_prefill(min(args.steps, 10), args.warmup)
     cpu = None if args.no_cpu else cpu_baseline_attention()
     line = {
         "metric": "prefill tokens/s per layer type + ms per 4k-token hybrid decision prefill",
@@ -392,7 +435,8 @@ def main():
         "cpu_baseline": cpu,
         "layers": {"attention_cfg1": attn, "gdn_cfg2": g2, "gdn_cfg0": g0},
         "hbm_ops": hbm,
-        "decision_prefill_ms_4k": None,
+        "decision_prefill_ms_4k": dec_ms,
+        "model_cfg3": dec,
     }
     print(json.dumps(line), flush=True)
     st.destroy()

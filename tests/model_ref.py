@@ -1,0 +1,64 @@
+"""Host restatement of the hybrid decoder prefill for the model-runner parity tests.
+
+The op sequence is the reference executor's (src/models/qwen3_5/native/src/model.rs:1119-1318);
+each op is the oracle's emulation of the corresponding reference kernel, and each GEMM is the
+float64 product of the bf16 operands rounded once to bf16 (cuBLASLt / hipBLASLt accumulate
+in float32, so single results may differ by one bf16 step)."""
+import numpy as np
+
+import oracle as O
+from qwen3_5_native import model as QM
+
+
+def gemm(x, w, M, N, K):
+    xf = O.bf16_to_f32(x).reshape(M, K).astype(np.float64)
+    wf = O.bf16_to_f32(w).reshape(N, K).astype(np.float64)
+    return O.f32_to_bf16((xf @ wf.T).astype(np.float32)).reshape(-1)
+
+
+def forward(m: QM.Model, ids) -> np.ndarray:
+    c = m.cfg
+    T = len(ids)
+    kd, vd = c.lin_k_heads * c.lin_k_dim, c.lin_v_heads * c.lin_v_dim
+    conv = 2 * kd + vd
+    gdn_w = conv + vd + 2 * c.lin_v_heads
+    attn_q = c.heads * c.head_dim * 2
+    attn_w = attn_q + 2 * c.kv_heads * c.head_dim
+    H, D, I = c.hidden, c.head_dim, c.intermediate
+    emb = m.tensor(QM.EMBED).reshape(c.vocab, H)
+    res = emb[np.asarray(ids)].reshape(-1).copy()
+    cs, sn = O.rotary_tables(np.arange(T, dtype=np.int64), c.rotary_half, c.rope_theta)
+    x = O.rms_norm(res, m.tensor(QM.INPUT_NORM, 0), T, H, c.eps)
+    for i in range(c.layers):
+        if not c.is_full(i):
+            gi = gemm(x, m.tensor(QM.GDN_IN, i), T, gdn_w, H)
+            q, k, v = O.gdn_conv(gi, gdn_w, m.tensor(QM.GDN_CONV, i), T, kd, vd)
+            beta, g = O.gdn_gates(gi[conv + vd:], gi[conv + vd + c.lin_v_heads:], gdn_w, m.tensor(QM.GDN_A_LOG, i),
+                                  m.tensor(QM.GDN_DT_BIAS, i), T, c.lin_v_heads)
+            o, _ = O.gdn_chunk_emul(q.reshape(-1), k.reshape(-1), v.reshape(-1), g.reshape(-1), beta.reshape(-1), T,
+                                    c.lin_v_heads, c.lin_k_heads, scale=c.lin_k_dim ** -0.5, want_state=False)
+            ln = O.gated_rms_norm(o.reshape(-1), gi[conv:], gdn_w, m.tensor(QM.GDN_NORM, i), T, c.lin_v_heads,
+                                  c.lin_v_dim, c.eps)
+            delta = gemm(ln, m.tensor(QM.GDN_OUT, i), T, H, vd)
+        else:
+            ai = gemm(x, m.tensor(QM.ATTN_QKV, i), T, attn_w, H)
+            q, gate, k = O.attn_prep(ai, ai[attn_q:], attn_w, m.tensor(QM.ATTN_Q_NORM, i),
+                                     m.tensor(QM.ATTN_K_NORM, i), cs, sn, T, c.heads, c.kv_heads, D,
+                                     c.rotary_half, c.eps)
+            ao = O.attention_emul(q.reshape(-1), k.reshape(-1), ai[attn_q + c.kv_heads * D:], attn_w,
+                                  gate.reshape(-1), T, c.heads, c.kv_heads, D, D ** -0.5)
+            delta = gemm(ao.reshape(-1), m.tensor(QM.ATTN_O, i), T, H, c.heads * D)
+        res, x = O.add_rms_norm(res, delta, m.tensor(QM.POST_NORM, i), T, H, c.eps)
+        gu = gemm(x, m.tensor(QM.MLP_GATE_UP, i), T, 2 * I, H)
+        act = O.silu_mul(gu, 2 * I, T, I)
+        delta = gemm(act.reshape(-1), m.tensor(QM.MLP_DOWN, i), T, H, I)
+        nxt = m.tensor(QM.INPUT_NORM, i + 1) if i + 1 < c.layers else m.tensor(QM.FINAL_NORM)
+        res, x = O.add_rms_norm(res, delta, nxt, T, H, c.eps)
+    return O.bf16_to_f32(np.asarray(x).reshape(T, H)[T - 1])
+
+
+def decide(m: QM.Model, last, labels) -> np.ndarray:
+    """cua_s1 executor.rs:61-78: float64 dots of embedding rows with the last hidden state."""
+    emb = m.tensor(QM.EMBED).reshape(m.cfg.vocab, m.cfg.hidden)
+    rows = O.bf16_to_f32(emb[np.asarray(labels)]).astype(np.float64)
+    return (rows @ np.asarray(last, np.float64)).astype(np.float32)

@@ -102,3 +102,18 @@ def test_error_strings(api):
     with pytest.raises(hip.HipError) as e:
         hip.check(INVALID, "attention")
     assert e.value.code == INVALID and "attention" in str(e.value)
+
+
+def test_model_library_exports_and_validates():
+    """libqwen3_5_model.so loads, exports the runner's symbols and rejects a bad config
+    before touching the device."""
+    import ctypes
+    from qwen3_5_native import model as QM
+
+    lib = QM.load()
+    for name in QM.SYMBOLS:
+        assert hasattr(lib, name), name
+    bad = QM._cfg(QM.Config(layers=2, hidden=512, intermediate=1024, vocab=100, heads=4, kv_heads=3))
+    h = ctypes.c_void_p()
+    assert lib.q35m_create(ctypes.byref(bad), 0, 16, ctypes.byref(h)) == hip.HIP_ERROR_INVALID_VALUE
+    assert lib.q35m_forward(None, None, 0, None) == hip.HIP_ERROR_INVALID_VALUE

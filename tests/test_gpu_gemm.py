@@ -1,0 +1,77 @@
+"""GPU parity of cs1_gemm (hipBLASLt, reference interface ops.h:117-124, gemm.cu:123-134):
+y [M, N] (rows of ldy) = x [M, K] w [N, K]^T, bf16 in and out, float32 accumulation."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import dev, empty, get_bf16, say, stream, ulp_diff
+from qwen3_5_native import hip
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gemm():
+    api = hip.api()
+    stream()
+    h = api.cs1_gemm_create(32 << 20)
+    assert h
+    yield h
+    api.cs1_gemm_destroy(h)
+
+
+def run(h, x, w, M, N, K, ldy=None, y_init=None):
+    api, st = hip.api(), stream()
+    ldy = ldy or N
+    dx, dw = dev(x), dev(w)
+    y = dev(y_init) if y_init is not None else empty(M * ldy * 2)
+    hip.check(api.cs1_gemm(h, dx.at(0), dw.at(0), y.at(0), M, N, K, ldy, st.handle), "gemm")
+    return get_bf16(y, M * ldy).reshape(M, ldy)
+
+
+def ref(x, w, M, N, K):
+    """float64 product of the bf16 values, rounded once to bfloat16."""
+    xf = O.bf16_to_f32(x).reshape(M, K).astype(np.float64)
+    wf = O.bf16_to_f32(w).reshape(N, K).astype(np.float64)
+    return O.f32_to_bf16((xf @ wf.T).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 256, 2560), (200, 512, 256), (4096, 2560, 9728 // 8), (37, 4168, 2560)])
+def test_gemm_matches_float64(gemm, M, N, K):
+    say(f"gemm M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K)
+    x = O.f32_to_bf16(rng.standard_normal(M * K).astype(np.float32))
+    w = O.f32_to_bf16((rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    got = run(gemm, x, w, M, N, K)
+    want = ref(x, w, M, N, K)
+    # float32 accumulation in another order than the float64 sum: one bf16 rounding step
+    # apart at most, except where the sum cancels to a tiny value
+    d = np.abs(O.bf16_to_f32(got).astype(np.float64) - O.bf16_to_f32(want).astype(np.float64))
+    scale = np.abs(O.bf16_to_f32(want)).max()
+    say(f"  max diff {d.max():.3e} of max |y| {scale:.3e}, ulp {ulp_diff(got[np.abs(O.bf16_to_f32(want)) > 1e-3 * scale], want[np.abs(O.bf16_to_f32(want)) > 1e-3 * scale])}")
+    assert d.max() <= 2 ** -7 * scale
+    assert ulp_diff(got[np.abs(O.bf16_to_f32(want)) > 1e-2 * scale], want[np.abs(O.bf16_to_f32(want)) > 1e-2 * scale]) <= 1
+
+
+def test_gemm_strided_output_and_repeatable(gemm):
+    """ldy > N fills a column slice of a wider buffer and leaves the rest untouched; a shape
+    reuses its plan, so repeated calls are bitwise identical (gemm.cu:1-10)."""
+    M, N, K, ldy = 130, 192, 512, 320
+    say(f"gemm strided M={M} N={N} K={K} ldy={ldy}")
+    rng = np.random.default_rng(5)
+    x = O.f32_to_bf16(rng.standard_normal(M * K).astype(np.float32))
+    w = O.f32_to_bf16((rng.standard_normal(N * K) * 0.05).astype(np.float32))
+    fill = np.full(M * ldy, 0x7F7F, np.uint16)
+    a = run(gemm, x, w, M, N, K, ldy, fill)
+    b = run(gemm, x, w, M, N, K, ldy, fill)
+    np.testing.assert_array_equal(a, b)
+    assert (a[:, N:] == 0x7F7F).all()
+    np.testing.assert_array_equal(a[:, :N], run(gemm, x, w, M, N, K))
+
+
+def test_gemm_edge_arguments(gemm):
+    api, st = hip.api(), stream()
+    say("gemm argument checks")
+    assert api.cs1_gemm(gemm, None, None, None, 0, 16, 16, 16, st.handle) == 0
+    assert api.cs1_gemm(gemm, None, None, None, 4, 16, 16, 8, st.handle) == hip.HIP_ERROR_INVALID_VALUE
+    assert api.cs1_gemm(None, None, None, None, 4, 16, 16, 16, st.handle) == hip.HIP_ERROR_INVALID_VALUE
