@@ -95,6 +95,10 @@ struct FaCfg {
     static constexpr int KS2 = BN / 32;            // 32-key steps of P V
     static constexpr int KLD = D + 8;              // bf16 row stride of K [BN][D]
     static constexpr int VLD = BN + 8;             // bf16 row stride of V^T [D][BN]
+    static constexpr int NCH = BN / 8;             // 16-byte key chunks per V^T row
+    // V^T layout: 16-byte key chunks in MFMA k order (64-key tiles), or key pairs with a
+    // pair swizzle (32-key tiles, where four chunks per row cannot spread the stores)
+    static constexpr bool CHUNKED = BN == 64;
     static constexpr int STAGE = BN * KLD + D * VLD;           // bf16 elements per stage
     static constexpr int BYTES = 4 * STAGE * 2;                // 2 groups x 2 stages
     static constexpr int KP = BN * D / 8 / GROUP_THREADS;      // K packs per thread
@@ -109,32 +113,70 @@ struct TileRegs {
 
 __device__ __forceinline__ u32x4 ldg16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// V^T column swizzle: key pair p of row d is stored at pair p ^ 2 ((d / 8) % 16) (within the
-// tile's pairs). Groups of four keys stay contiguous, and the transposing stores of one
-// wave (rows 8c + 2e, c = 0..15) spread over all 64 banks.
+// Chunked V^T layout (64-key tiles). Row d holds the tile's keys in the MFMA's k order:
+// within each 32-key step s2,
+// lane group g's eight keys {4g .. 4g+3, 16+4g .. 16+4g+3} form one 16-byte chunk
+// c = 4 s2 + g, so a lane's A operand of V^T P^T is a single 16-byte read. Chunk c of row d
+// sits at slot c ^ ((d / 8) mod NCH): the transposing stores of one wave (rows 8c + 2e)
+// spread over the banks, and since the XOR only mixes d / 8 into the chunk bits, a reader's
+// address is one of two per-lane bases (by the parity of its 16-row block) plus a constant.
+template <int D>
+__device__ __forceinline__ int vt_slot(int d, int chunk) {
+    return chunk ^ ((d >> 3) & (FaCfg<D>::NCH - 1));
+}
+
+// Pair layout (32-key tiles): key pair p of row d is stored at pair p ^ 2 ((d / 8) % 8):
+// groups of four keys stay contiguous, and the transposing stores of one wave
+// (rows 8c + 2e) spread over the banks.
 template <int D>
 __device__ __forceinline__ int vt_pair(int d, int pair) {
     return pair ^ ((((d >> 3) & 15) << 1) & (FaCfg<D>::BN / 2 - 1));
 }
 
+// element offset, within row d, of key j of the tile (j even: the pair j, j + 1 is one word)
+template <int D>
+__device__ __forceinline__ int vt_pos(int d, int j) {
+    if (FaCfg<D>::CHUNKED) {
+        const int jj = j & 31, chunk = 4 * (j >> 5) + ((jj & 15) >> 2), e = (jj & 3) + (jj & 16 ? 4 : 0);
+        return 8 * vt_slot<D>(d, chunk) + e;
+    }
+    return 2 * vt_pair<D>(d, j >> 1);
+}
+
+// Buffer descriptor over rows [k0, T) of a row-major bf16 tensor with row stride ld and
+// rows of D elements: rows at or past T fall outside the descriptor and read as zero (those
+// keys are masked, and their probabilities are exactly zero). Based at row k0, so every
+// offset stays small whatever T is.
+template <int D>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const bf16* base, int ld, int k0, int T) {
+    const uint64_t a = (uint64_t)(base + (size_t)k0 * ld);
+    const uint64_t ua = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a) |
+                        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) << 32);
+    const int rows = min(T - k0, FaCfg<D>::BN);
+    const int bytes = rows > 0 ? ((rows - 1) * ld + D) * 2 : 0;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)ua, (short)0, __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int voff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+
 template <int D>
 __device__ __forceinline__ void load_tile(TileRegs<D>& r, const bf16* __restrict__ k, const bf16* __restrict__ v,
                                           int ldk, int ldv, int k0, int T, int tg) {
+    const __amdgpu_buffer_rsrc_t kr = tile_rsrc<D>(k, ldk, k0, T), vr = tile_rsrc<D>(v, ldv, k0, T);
 #pragma unroll
     for (int i = 0; i < FaCfg<D>::KP; i++) {
         const int x = tg + i * GROUP_THREADS;
-        const int row = x / (D / 8), col = (x % (D / 8)) * 8, s = min(k0 + row, T - 1);
-        r.k[i] = ldg16(k + (size_t)s * ldk + col);
+        const int row = x / (D / 8), col = (x % (D / 8)) * 8;
+        r.k[i] = bload16(kr, (row * ldk + col) * 2);
     }
 #pragma unroll
     for (int i = 0; i < FaCfg<D>::VP; i++) {
         const int x = tg + i * GROUP_THREADS;
         const int pair = x / (D / 8), col = (x % (D / 8)) * 8;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int s = min(k0 + 2 * pair + j, T - 1);  // rows past T are masked out
-            r.v[i][j] = ldg16(v + (size_t)s * ldv + col);
-        }
+        for (int j = 0; j < 2; j++) r.v[i][j] = bload16(vr, ((2 * pair + j) * ldv + col) * 2);
     }
 }
 
@@ -158,8 +200,8 @@ __device__ __forceinline__ void store_tile(const TileRegs<D>& r, bf16* ks, int t
             const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);
             const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);
             const int d0 = col + 2 * e, d1 = d0 + 1;
-            *reinterpret_cast<uint32_t*>(vt + d0 * FaCfg<D>::VLD + 2 * vt_pair<D>(d0, pair)) = lo;
-            *reinterpret_cast<uint32_t*>(vt + d1 * FaCfg<D>::VLD + 2 * vt_pair<D>(d1, pair)) = hi;
+            *reinterpret_cast<uint32_t*>(vt + d0 * FaCfg<D>::VLD + vt_pos<D>(d0, 2 * pair)) = lo;
+            *reinterpret_cast<uint32_t*>(vt + d1 * FaCfg<D>::VLD + vt_pos<D>(d1, 2 * pair)) = hi;
         }
     }
 }
@@ -246,6 +288,22 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
         const bf16* vt = ks + BN * Cfg::KLD;
         if (live) {
             const int k0 = tile * BN;
+            // V^T fragment (dt, s2) of this lane: row d = 16 dt + col; chunked layout: chunk
+            // 4 s2 + grp at slot (4 s2 + grp) ^ ((2 dt + col / 8) mod NCH), i.e. a per-lane base for
+            // each parity of dt plus a constant.
+            auto read_v = [&](int dt, int s2) {
+                if (Cfg::CHUNKED) {
+                    const bf16* vr =
+                        vt + (16 * dt + col) * Cfg::VLD + 8 * (grp ^ (((col >> 3) | ((dt & 1) << 1)) & 3));
+                    return *reinterpret_cast<const u32x4*>(vr + 32 * (s2 ^ ((dt >> 1) & 1)));
+                }
+                // keys 32 s2 + 4 grp .. + 3 and 32 s2 + 16 + 4 grp .. + 3
+                const int d = 16 * dt + col;
+                const bf16* vr = vt + d * Cfg::VLD;
+                const u32x2 a0 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair<D>(d, 16 * s2 + 2 * grp));
+                const u32x2 a1 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair<D>(d, 16 * s2 + 8 + 2 * grp));
+                return u32x4{a0[0], a0[1], a1[0], a1[1]};
+            };
             // S^T = K Q^T: NSUB sub-tiles of 16 keys x QT query tiles
             f32x4 st[Cfg::NSUB][QT];
 #pragma unroll
@@ -310,19 +368,13 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
             }
             // O^T += V^T P^T; each V^T fragment feeds every query tile
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) {
-                const int d = 16 * dt + col;
-                const bf16* vr = vt + d * Cfg::VLD;
+            for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int s2 = 0; s2 < Cfg::KS2; s2++) {
-                    // keys 32 s2 + 4 grp .. + 3 and 32 s2 + 16 + 4 grp .. + 3
-                    const u32x2 a0 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair<D>(d, 16 * s2 + 2 * grp));
-                    const u32x2 a1 = *reinterpret_cast<const u32x2*>(vr + 2 * vt_pair<D>(d, 16 * s2 + 8 + 2 * grp));
-                    const u32x4 a = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                    const u32x4 a = read_v(dt, s2);
 #pragma unroll
                     for (int qt = 0; qt < QT; qt++) o[qt][dt] = mfma16(a, pf[qt][s2], o[qt][dt]);
                 }
-            }
         }
         // next tile of each group: registers to the other stage, then fetch the one after
         if (it + 1 < nt0) {
