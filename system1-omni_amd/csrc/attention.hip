@@ -272,6 +272,10 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
     const int ntg = grp_id == 0 ? nt0 : ntiles / 2;  // this group's tiles
     bf16* gstage = lds + grp_id * 2 * Cfg::STAGE;
 
+    // Pipeline, one barrier per step: at step it a group first stores its tile it + 1 (in
+    // registers since the previous step) to its other stage and issues the loads of tile
+    // it + 2, then computes tile it. The barrier closing step it - 1 guarantees nobody still
+    // reads that other stage, and the one closing step it publishes tile it + 1.
     TileRegs<D> regs;
     if (ntg > 0) {
         load_tile<D>(regs, kh, vh, ldk, ldv, grp_id * BN, T, tg);
@@ -279,9 +283,12 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
         store_tile<D>(regs, gstage, tg);
         if (ntg > 1) load_tile<D>(regs, kh, vh, ldk, ldv, (2 + grp_id) * BN, T, tg);
     }
-    wait_vm_all();
     __syncthreads();
     for (int it = 0; it < nt0; it++) {
+        if (it + 1 < ntg) {
+            store_tile<D>(regs, gstage + ((it + 1) & 1) * Cfg::STAGE, tg);
+            if (it + 2 < ntg) load_tile<D>(regs, kh, vh, ldk, ldv, (2 * (it + 2) + grp_id) * BN, T, tg);
+        }
         const int tile = 2 * it + grp_id;
         const bool live = it < ntg;  // wave-uniform
         const bf16* ks = gstage + (it & 1) * Cfg::STAGE;
@@ -376,15 +383,7 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
                     for (int qt = 0; qt < QT; qt++) o[qt][dt] = mfma16(a, pf[qt][s2], o[qt][dt]);
                 }
         }
-        // next tile of each group: registers to the other stage, then fetch the one after
-        if (it + 1 < nt0) {
-            __syncthreads();  // both groups are done with their other stage
-            if (it + 1 < ntg) {
-                store_tile<D>(regs, gstage + ((it + 1) & 1) * Cfg::STAGE, tg);
-                if (it + 2 < ntg) load_tile<D>(regs, kh, vh, ldk, ldv, (2 * (it + 2) + grp_id) * BN, T, tg);
-            }
-            __syncthreads();
-        }
+        __syncthreads();
     }
 
     // merge the two groups' partial states through LDS: group 1 publishes, group 0 finishes
