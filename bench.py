@@ -272,6 +272,43 @@ def bench_decision_prefill(steps, warmup, T=4096):
                 "frac_of_bf16_peak": flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
 
+def bench_candidates(steps, warmup, P=2048, n=8):
+    """the random-init 27B-class hybrid decoder (64 layers, 3:1, hidden
+    5120, 24/4 x 256 attention, GDN 16 qk / 48 v heads, SwiGLU 17408, vocabulary 248320, untied
+    LM head). A step captures a 2048-token prefix, then scores 8 candidate continuations of
+    U[64, 256] tokens (seeded) packed into one pass from the shared prefix state, returning
+    each candidate's summed token log-probability; wall-clock ms, with the capture and the
+    scoring pass also timed apart."""
+    from qwen3_5_native import model as QM
+
+    cfg = QM.CFG4_27B
+    rng = np.random.default_rng(6)
+    prefix = rng.integers(0, cfg.vocab, P).astype(np.int32)
+    lens = rng.integers(64, 257, n)
+    cands = [rng.integers(0, cfg.vocab, int(k)).astype(np.int32) for k in lens]
+    m = QM.Model(cfg, seed=0, max_tokens=P + 256 if sum(lens) <= P + 256 else int(sum(lens)))
+    try:
+        for _ in range(max(warmup, 1)):
+            m.capture(prefix)
+            scores = m.score(cands)
+        cap = sco = 0.0
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            m.capture(prefix)
+            t1 = time.perf_counter()
+            scores = m.score(cands)
+            t2 = time.perf_counter()
+            cap += t1 - t0
+            sco += t2 - t1
+    finally:
+        m.close()
+    return {"workload": "cfg4 random-init 27B-class hybrid decoder (64 layers), 2048-token prefix captured, "
+                        f"{n} candidates of {', '.join(str(int(k)) for k in lens)} tokens scored from it",
+            "ms_per_job": (cap + sco) * 1e3 / steps, "capture_ms": cap * 1e3 / steps, "score_ms": sco * 1e3 / steps,
+            "candidate_tokens": int(sum(lens)), "best_candidate": int(np.argmax(scores)),
+            "scores": [round(float(x), 3) for x in scores]}
+
+
 def cpu_baseline_attention():
     """The oracle's emulation of the reference flash kernel (C, OpenMP) on this host, over
     the full config-1 layer, repeated until about 10 s of work."""
@@ -423,6 +460,7 @@ def main():
                    "cfg0 GDN chunked prefill T=512 H=HK=16 D=128, S0=0")
     hbm = bench_hbm_ops(api, st, ev, args.steps, args.warmup)
     dec_ms, dec = (None, None) if args.no_model else bench_decision_prefill(min(args.steps, 10), args.warmup)
+    cand = None if args.no_model else bench_candidates(min(args.steps, 3), 1)
     cpu = None if args.no_cpu else cpu_baseline_attention()
     line = {
         "metric": "prefill tokens/s per layer type + ms per 4k-token hybrid decision prefill",
@@ -437,6 +475,7 @@ def main():
         "hbm_ops": hbm,
         "decision_prefill_ms_4k": dec_ms,
         "model_cfg3": dec,
+        "model_cfg4": cand,
     }
     print(json.dumps(line), flush=True)
     st.destroy()

@@ -37,6 +37,7 @@ typedef struct Q35ModelConfig {
     int lin_k_dim, lin_v_dim;      /* Gated DeltaNet head dims (128) */
     int full_attention_interval; /* layer i is full attention when (i + 1) % interval == 0 */
     float eps;                   /* RMSNorm epsilon */
+    int lm_head;                 /* 1: a separate [vocab, hidden] LM head for token log-probabilities */
 } Q35ModelConfig;
 
 /* Weight tensors, for tests that rebuild the forward on the host. */
@@ -56,7 +57,8 @@ enum {
     Q35M_ATTN_K_NORM = 12, /* [Dh] */
     Q35M_ATTN_O = 13,     /* [hidden, Hq Dh] */
     Q35M_MLP_GATE_UP = 14, /* [2 I, hidden]: gate rows then up rows */
-    Q35M_MLP_DOWN = 15    /* [hidden, I] */
+    Q35M_MLP_DOWN = 15,   /* [hidden, I] */
+    Q35M_LM_HEAD = 16     /* [vocab, hidden] (lm_head = 1) */
 };
 
 /* Allocate and initialise a model for prompts of up to max_tokens tokens. */
@@ -73,6 +75,26 @@ int q35m_forward(void* model, const int32_t* ids, int T, float* last_hidden);
 
 /* forward, then logits[i] = float64 dot(embedding row label_ids[i], last hidden). */
 int q35m_decide(void* model, const int32_t* ids, int T, const int32_t* label_ids, int n_labels, float* logits);
+
+/* Prefix branching (the reference executor's capture / continue pair, model.rs:952-1073 and
+ * run_window 1352-1571, with the candidate scoring of src/models/lfm2/engine.py:128-146).
+ *
+ * q35m_capture runs prompt rows [0, P) (P a positive multiple of 64) and keeps, per layer,
+ * the state a continuation needs: post-prep K and raw V rows of each attention layer, the
+ * float32 final state and the last three pre-conv rows of each Gated DeltaNet layer, and the
+ * final-norm hidden state of row P - 1.
+ *
+ * q35m_score continues that prefix with n candidates packed into one pass (the GEMMs,
+ * norms and MLP over all candidate rows; conv, the delta rule and attention per candidate
+ * from the shared prefix state), and returns per candidate the summed log-probability of
+ * its tokens: scores[c] = sum_j log softmax(lm_head h_{P-1+j})[ids_c[j]], h_{P-1} being the
+ * prefix's last row. Requires lm_head = 1 and a preceding capture on this model. */
+int q35m_capture(void* model, const int32_t* ids, int P);
+int q35m_score(void* model, const int32_t* ids, const int32_t* lens, int n, double* scores);
+
+/* Full forward of one prompt and the log-probability of each next token:
+ * logprobs[t] = log softmax(lm_head h_t)[ids[t + 1]] for t < T - 1 (requires lm_head = 1). */
+int q35m_logprobs(void* model, const int32_t* ids, int T, float* logprobs);
 
 /* Device address and element count of a weight tensor (layer ignored for model-wide ones);
  * returns hipErrorInvalidValue if the layer has no such tensor. */

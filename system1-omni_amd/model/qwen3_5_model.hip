@@ -12,13 +12,17 @@
 //     gate_up = x W_gu^T; act = silu(gate) up; delta = act W_down^T        (1301-1315)
 //     res += delta, x = rms_norm(res, next layer's input_norm or final_norm) (1316-1332)
 //   last hidden = x[T - 1] as float32                                       (1100-1115)
-// and the decision head of src/models/cua_s1/native/src/executor.rs:61-78 (float64 dot
-// products of embedding rows with the last hidden state).
+// the decision head of src/models/cua_s1/native/src/executor.rs:61-78 (float64 dot
+// products of embedding rows with the last hidden state), and prefix branching: capture of a
+// prompt prefix and the continuation of several candidates from it (run_window 1352-1571),
+// scored by summed token log-probabilities (src/models/lfm2/engine.py:128-146).
 //
-// Memory: the weights live in one device allocation (about 8 GB for the 4B-class
-// configuration), the per-prompt buffers in a second one sized for max_tokens.
+// Memory: the weights live in one device allocation (about 8 GB for the 4B-class and 54 GB
+// for the 27B-class configuration), the per-prompt buffers in a second one sized for
+// max_tokens, a captured prefix in a third.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -34,7 +38,7 @@ constexpr size_t BF16 = 2;
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-// ---------------------------------------------------------------- device initialisation
+// ---------------------------------------------------------------- device kernels
 
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
     z += 0x9e3779b97f4a7c15ull;
@@ -50,6 +54,8 @@ __device__ __forceinline__ uint16_t bf16_rne(float x) {
     const uint32_t u = __float_as_uint(x);
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
+
+__device__ __forceinline__ float bf16_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
 enum Fill { FILL_NORMAL = 0, FILL_CONST = 1, FILL_LOG_UNIFORM16 = 2 };
 
@@ -74,6 +80,53 @@ __global__ void fill_kernel(uint16_t* p, size_t n, uint64_t key, int kind, float
     }
 }
 
+template <int OP>
+__device__ __forceinline__ float block_reduce(float v, float* red) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const float w = __shfl_xor(v, o, 64);
+        v = OP == 0 ? fmaxf(v, w) : v + w;
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    v = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) v = OP == 0 ? fmaxf(v, red[i]) : v + red[i];
+    return v;
+}
+
+// out[r] = log softmax(logits[r, :])[target[r]] in float32 from bfloat16 logits (the
+// reference scores `logits.float().log_softmax(-1)` gathered at the target). One block per
+// row; V a multiple of 8 (16-byte loads).
+__global__ void __launch_bounds__(256) logprob_kernel(const uint16_t* __restrict__ logits, int V,
+                                                      const int32_t* __restrict__ target, float* __restrict__ out) {
+    __shared__ float red[4];
+    const uint4* row = reinterpret_cast<const uint4*>(logits + (size_t)blockIdx.x * V);
+    const int n8 = V / 8;
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < n8; i += 256) {
+        const uint4 p = row[i];
+        const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            mx = fmaxf(mx, fmaxf(__uint_as_float(w[e] << 16), __uint_as_float(w[e] & 0xffff0000u)));
+    }
+    mx = block_reduce<0>(mx, red);
+    float s = 0.f;
+    for (int i = threadIdx.x; i < n8; i += 256) {
+        const uint4 p = row[i];
+        const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            s += expf(__uint_as_float(w[e] << 16) - mx) + expf(__uint_as_float(w[e] & 0xffff0000u) - mx);
+    }
+    s = block_reduce<1>(s, red);
+    if (threadIdx.x == 0) {
+        const float t = bf16_f32(logits[(size_t)blockIdx.x * V + target[blockIdx.x]]);
+        out[blockIdx.x] = t - mx - logf(s);
+    }
+}
+
 // ---------------------------------------------------------------- model
 
 struct Tensor {
@@ -89,12 +142,21 @@ struct Layer {
 };
 
 struct Widths {
-    size_t kd, vd, conv, gdn_in, attn_q, attn_in;
+    size_t kd, vd, conv, gdn_in, attn_q, attn_in, kv;
 };
 
 struct Scratch {
     size_t ids, res, x, delta, gdn_in, lq, lk, lv, lo, ln, beta, g, ws, attn_in, aq, agate, ak, ao, gate_up, act,
-        cos, sin, total;
+        cos, sin, ccos, csin, kwin, vwin, cst, cq, ck, cv, hs, tgt, logits, lp, total;
+};
+
+// Per-layer state of a captured prompt prefix (offsets into the prefix allocation).
+struct Prefix {
+    int len = 0;
+    unsigned char* mem = nullptr;
+    std::vector<size_t> k, v;        // per attention layer: [len, Hk Dh] post-prep K, raw V
+    std::vector<size_t> state, tail; // per GDN layer: float32 [Hv, 128, 128], 3 pre-conv rows
+    size_t last = 0;                 // final-norm hidden state of row len - 1
 };
 
 struct Model {
@@ -106,15 +168,23 @@ struct Model {
     unsigned char* weights = nullptr;
     unsigned char* scratch = nullptr;
     Scratch s{};
-    Tensor embed, final_norm;
+    Tensor embed, final_norm, lm_head;
     std::vector<Layer> layers;
     bool graph_enabled = false;
     std::map<int, void*> graphs;  // prompt length -> executable graph
     int cos_len = 0;              // positions held by the rotary tables
+    Prefix pre;
 };
 
+// The packed candidates of a scoring pass: rows off[c] .. off[c] + len[c] - 1.
+struct Cands {
+    std::vector<int> off, len;
+};
+
+enum Mode { PLAIN = 0, CAPTURE = 1, CANDIDATES = 2 };
+
 void* at(Model& m, const Tensor& t) { return m.weights + t.off; }
-void* sc(Model& m, size_t off, size_t row_bytes = 0, size_t row = 0) { return m.scratch + off + row * row_bytes; }
+unsigned char* sc(Model& m, size_t off) { return m.scratch + off; }
 
 #define TRY(x)                          \
     do {                                \
@@ -124,10 +194,10 @@ void* sc(Model& m, size_t off, size_t row_bytes = 0, size_t row = 0) { return m.
 
 bool valid(const Q35ModelConfig& c) {
     return c.layers > 0 && c.hidden > 0 && c.hidden % 8 == 0 && c.intermediate > 0 && c.intermediate % 8 == 0 &&
-           c.vocab > 0 && c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0 && c.head_dim == 256 &&
-           c.rotary_half > 0 && 2 * c.rotary_half <= c.head_dim && c.lin_k_heads > 0 && c.lin_v_heads > 0 &&
-           c.lin_v_heads % c.lin_k_heads == 0 && c.lin_k_dim == 128 && c.lin_v_dim == 128 &&
-           c.full_attention_interval > 0 && c.eps > 0.f && c.rope_theta > 0.0;
+           c.vocab > 0 && c.vocab % 8 == 0 && c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0 &&
+           c.head_dim == 256 && c.rotary_half > 0 && 2 * c.rotary_half <= c.head_dim && c.lin_k_heads > 0 &&
+           c.lin_v_heads > 0 && c.lin_v_heads % c.lin_k_heads == 0 && c.lin_k_dim == 128 && c.lin_v_dim == 128 &&
+           c.full_attention_interval > 0 && c.eps > 0.f && c.rope_theta > 0.0 && (c.lm_head == 0 || c.lm_head == 1);
 }
 
 int fill(Model& m, const Tensor& t, uint64_t key, int kind, float value) {
@@ -138,30 +208,39 @@ int fill(Model& m, const Tensor& t, uint64_t key, int kind, float value) {
     return hipGetLastError();
 }
 
-// Rotary tables for positions 0 .. T-1 as the reference computes them on the host
+uint16_t host_bf16(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Rotary tables for the given positions as the reference computes them on the host
 // (src/models/qwen3_5/native/src/inputs.rs:75-93, all three position axes equal for text):
 // float32 inverse frequencies theta^(-2i / (2 half)), float32 angle, float64 cos / sin,
 // rounded to bfloat16.
-int rotary(Model& m, int T) {
+int rotary_rows(Model& m, const std::vector<int>& pos, size_t cos_off, size_t sin_off) {
     const int half = m.cfg.rotary_half;
     std::vector<float> inv(half);
     for (int i = 0; i < half; i++)
         inv[i] = 1.f / powf((float)m.cfg.rope_theta, (float)(2 * i) / (float)(2 * half));
-    std::vector<uint16_t> c((size_t)T * half), s((size_t)T * half);
-    auto rne = [](float x) {
-        uint32_t u;
-        std::memcpy(&u, &x, 4);
-        return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-    };
-    for (int t = 0; t < T; t++)
+    std::vector<uint16_t> c(pos.size() * half), s(pos.size() * half);
+    for (size_t t = 0; t < pos.size(); t++)
         for (int i = 0; i < half; i++) {
-            const double a = (double)(inv[i] * (float)t);
-            c[(size_t)t * half + i] = rne((float)std::cos(a));
-            s[(size_t)t * half + i] = rne((float)std::sin(a));
+            const double a = (double)(inv[i] * (float)pos[t]);
+            c[t * half + i] = host_bf16((float)std::cos(a));
+            s[t * half + i] = host_bf16((float)std::sin(a));
         }
-    TRY(cs1_upload(sc(m, m.s.cos), c.data(), c.size() * 2, m.stream));
-    TRY(cs1_upload(sc(m, m.s.sin), s.data(), s.size() * 2, m.stream));
-    m.cos_len = T;
+    TRY(cs1_upload(sc(m, cos_off), c.data(), c.size() * 2, m.stream));
+    TRY(cs1_upload(sc(m, sin_off), s.data(), s.size() * 2, m.stream));
+    return 0;
+}
+
+int rotary(Model& m) {
+    if (m.cos_len >= m.max_tokens) return 0;
+    std::vector<int> pos(m.max_tokens);
+    for (int t = 0; t < m.max_tokens; t++) pos[t] = t;
+    TRY(rotary_rows(m, pos, m.s.cos, m.s.sin));
+    m.cos_len = m.max_tokens;
     return 0;
 }
 
@@ -170,87 +249,141 @@ int gemm(Model& m, size_t x, const Tensor& wt, size_t y, int T, int N, int K) {
     return cs1_gemm(m.gemm, sc(m, x), at(m, wt), sc(m, y), T, N, K, N, m.stream);
 }
 
-// The layer stack on embedded rows (res already holds the embeddings).
-int run(Model& m, int T) {
+// The layer stack on T embedded rows (res holds the embeddings). PLAIN: one prompt from
+// position 0. CAPTURE: the same, keeping the per-layer prefix state in m.pre. CANDIDATES:
+// rows are the packed candidates, each continuing the captured prefix at position pre.len.
+int run(Model& m, int T, Mode mode, const Cands* cd) {
     const Q35ModelConfig& c = m.cfg;
     const Widths& w = m.w;
+    const Scratch& s = m.s;
     const int hv = c.lin_v_heads, hq = c.heads, hk = c.kv_heads, hd = c.head_dim;
+    const size_t gw = w.gdn_in * BF16, aw = w.attn_in * BF16, qrow = (size_t)hq * hd * BF16, kvb = w.kv * BF16;
+    const int P = m.pre.len;
     void* st = m.stream;
-    TRY(cs1_rms_norm(sc(m, m.s.res), at(m, m.layers[0].input_norm), sc(m, m.s.x), T, c.hidden, c.eps, st));
+    const float gdn_scale = powf((float)c.lin_k_dim, -0.5f), att_scale = powf((float)hd, -0.5f);
+    TRY(cs1_rms_norm(sc(m, s.res), at(m, m.layers[0].input_norm), sc(m, s.x), T, c.hidden, c.eps, st));
+    int ai = 0, li = 0;
     for (size_t i = 0; i < m.layers.size(); i++) {
         const Layer& L = m.layers[i];
         if (!L.full) {
             const int ld = (int)w.gdn_in;
-            TRY(gemm(m, m.s.x, L.gdn_in, m.s.gdn_in, T, (int)w.gdn_in, c.hidden));
-            unsigned char* base = static_cast<unsigned char*>(sc(m, m.s.gdn_in));
+            TRY(gemm(m, s.x, L.gdn_in, s.gdn_in, T, (int)w.gdn_in, c.hidden));
+            unsigned char* base = sc(m, s.gdn_in);
             unsigned char* z = base + w.conv * BF16;
             unsigned char* b = z + w.vd * BF16;
             unsigned char* a = b + hv * BF16;
-            TRY(cs1_gdn_conv(base, ld, at(m, L.conv), sc(m, m.s.lq), sc(m, m.s.lk), sc(m, m.s.lv), T, (int)w.kd,
-                             (int)w.vd, st));
-            TRY(cs1_gdn_gates(b, a, ld, at(m, L.a_log), at(m, L.dt_bias), sc(m, m.s.beta),
-                              static_cast<float*>(sc(m, m.s.g)), T, hv, st));
-            TRY(cs1_gdn_prefill(sc(m, m.s.lq), sc(m, m.s.lk), sc(m, m.s.lv), static_cast<const float*>(sc(m, m.s.g)),
-                                sc(m, m.s.beta), sc(m, m.s.lo), static_cast<float*>(sc(m, m.s.ws)), T, hv,
-                                c.lin_k_heads, powf((float)c.lin_k_dim, -0.5f), st));
-            TRY(cs1_gated_rms_norm(sc(m, m.s.lo), z, ld, at(m, L.gnorm), sc(m, m.s.ln), T, hv, c.lin_v_dim, c.eps,
-                                   st));
-            TRY(gemm(m, m.s.ln, L.gout, m.s.delta, T, c.hidden, (int)w.vd));
+            TRY(cs1_gdn_gates(b, a, ld, at(m, L.a_log), at(m, L.dt_bias), sc(m, s.beta),
+                              reinterpret_cast<float*>(sc(m, s.g)), T, hv, st));
+            if (mode == CANDIDATES) {
+                // each candidate: three restored prefix rows ahead of its own rows, so the
+                // convolution sees its full history (those three outputs are not used), then
+                // the delta rule from the prefix's final state (model.rs:1421-1470)
+                for (size_t k = 0; k < cd->off.size(); k++) {
+                    const int off = cd->off[k], len = cd->len[k];
+                    TRY(cs1_copy_dd(sc(m, s.cst), m.pre.mem + m.pre.tail[li], 3 * gw, st));
+                    TRY(cs1_copy_dd(sc(m, s.cst) + 3 * gw, base + off * gw, (size_t)len * gw, st));
+                    TRY(cs1_gdn_conv(sc(m, s.cst), ld, at(m, L.conv), sc(m, s.cq), sc(m, s.ck), sc(m, s.cv), len + 3,
+                                     (int)w.kd, (int)w.vd, st));
+                    TRY(cs1_gdn_prefill_x(sc(m, s.cq) + 3 * w.kd * BF16, sc(m, s.ck) + 3 * w.kd * BF16,
+                                          sc(m, s.cv) + 3 * w.vd * BF16,
+                                          reinterpret_cast<const float*>(sc(m, s.g)) + (size_t)off * hv,
+                                          sc(m, s.beta) + (size_t)off * hv * BF16, sc(m, s.lo) + off * w.vd * BF16,
+                                          reinterpret_cast<float*>(sc(m, s.ws)), len, hv, c.lin_k_heads, gdn_scale,
+                                          m.pre.mem + m.pre.state[li], nullptr, st));
+                }
+            } else {
+                TRY(cs1_gdn_conv(base, ld, at(m, L.conv), sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), T, (int)w.kd,
+                                 (int)w.vd, st));
+                TRY(cs1_gdn_prefill_x(sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), reinterpret_cast<const float*>(sc(m, s.g)),
+                                      sc(m, s.beta), sc(m, s.lo), reinterpret_cast<float*>(sc(m, s.ws)), T, hv,
+                                      c.lin_k_heads, gdn_scale, nullptr,
+                                      mode == CAPTURE ? m.pre.mem + m.pre.state[li] : nullptr, st));
+                if (mode == CAPTURE)  // the last three pre-conv rows (model.rs:1427-1434)
+                    TRY(cs1_copy_dd(m.pre.mem + m.pre.tail[li], base + (size_t)(T - 3) * gw, 3 * gw, st));
+            }
+            TRY(cs1_gated_rms_norm(sc(m, s.lo), z, ld, at(m, L.gnorm), sc(m, s.ln), T, hv, c.lin_v_dim, c.eps, st));
+            TRY(gemm(m, s.ln, L.gout, s.delta, T, c.hidden, (int)w.vd));
+            li++;
         } else {
             const int ld = (int)w.attn_in;
-            TRY(gemm(m, m.s.x, L.qkv, m.s.attn_in, T, (int)w.attn_in, c.hidden));
-            unsigned char* base = static_cast<unsigned char*>(sc(m, m.s.attn_in));
+            TRY(gemm(m, s.x, L.qkv, s.attn_in, T, (int)w.attn_in, c.hidden));
+            unsigned char* base = sc(m, s.attn_in);
             unsigned char* k = base + w.attn_q * BF16;
-            unsigned char* v = k + (size_t)hk * hd * BF16;
-            TRY(cs1_attn_prep(base, k, ld, at(m, L.q_norm), at(m, L.k_norm), sc(m, m.s.cos), sc(m, m.s.sin),
-                              sc(m, m.s.aq), sc(m, m.s.agate), sc(m, m.s.ak), T, hq, hk, hd, c.rotary_half, c.eps,
-                              st));
-            TRY(cs1_attention_gated(sc(m, m.s.aq), sc(m, m.s.ak), v, ld, sc(m, m.s.agate), sc(m, m.s.ao), T, hq, hk,
-                                    hd, powf((float)hd, -0.5f), st));
-            TRY(gemm(m, m.s.ao, L.o, m.s.delta, T, c.hidden, hq * hd));
+            unsigned char* v = k + kvb;
+            const size_t co = mode == CANDIDATES ? s.ccos : s.cos, so = mode == CANDIDATES ? s.csin : s.sin;
+            TRY(cs1_attn_prep(base, k, ld, at(m, L.q_norm), at(m, L.k_norm), sc(m, co), sc(m, so), sc(m, s.aq),
+                              sc(m, s.agate), sc(m, s.ak), T, hq, hk, hd, c.rotary_half, c.eps, st));
+            if (mode == CANDIDATES) {
+                // each candidate: keys [prefix K/V | its own], queries its own rows at q_base = P
+                // (the pointers of q, gate and out are based P rows ahead of the candidate;
+                // rows below q_base are never touched) (model.rs:1495-1554)
+                for (size_t j = 0; j < cd->off.size(); j++) {
+                    const int off = cd->off[j], len = cd->len[j];
+                    TRY(cs1_copy_dd(sc(m, s.kwin), m.pre.mem + m.pre.k[ai], (size_t)P * kvb, st));
+                    TRY(cs1_copy_dd(sc(m, s.kwin) + (size_t)P * kvb, sc(m, s.ak) + (size_t)off * kvb, (size_t)len * kvb,
+                                    st));
+                    TRY(cs1_copy_dd(sc(m, s.vwin), m.pre.mem + m.pre.v[ai], (size_t)P * kvb, st));
+                    TRY(cs1_copy2d(sc(m, s.vwin) + (size_t)P * kvb, kvb, v + (size_t)off * aw, aw, kvb, len, st));
+                    const ptrdiff_t q0 = ((ptrdiff_t)off - P) * (ptrdiff_t)qrow;
+                    TRY(cs1_attention_gated_prefix(sc(m, s.aq) + q0, sc(m, s.kwin), sc(m, s.vwin), (int)w.kv,
+                                                   sc(m, s.agate) + q0, sc(m, s.ao) + q0, P + len, hq, hk, hd,
+                                                   att_scale, P, st));
+                }
+            } else {
+                if (mode == CAPTURE) {  // post-prep K, raw V (model.rs:1527-1531)
+                    TRY(cs1_copy_dd(m.pre.mem + m.pre.k[ai], sc(m, s.ak), (size_t)T * kvb, st));
+                    TRY(cs1_copy2d(m.pre.mem + m.pre.v[ai], kvb, v, aw, kvb, T, st));
+                }
+                TRY(cs1_attention_gated(sc(m, s.aq), sc(m, s.ak), v, ld, sc(m, s.agate), sc(m, s.ao), T, hq, hk, hd,
+                                        att_scale, st));
+            }
+            TRY(gemm(m, s.ao, L.o, s.delta, T, c.hidden, hq * hd));
+            ai++;
         }
-        TRY(cs1_add_rms_norm(sc(m, m.s.res), sc(m, m.s.delta), at(m, L.post_norm), sc(m, m.s.x), T, c.hidden, c.eps,
-                             st));
-        TRY(gemm(m, m.s.x, L.gate_up, m.s.gate_up, T, 2 * c.intermediate, c.hidden));
-        TRY(cs1_silu_mul(sc(m, m.s.gate_up), 2 * c.intermediate, sc(m, m.s.act), T, c.intermediate, st));
-        TRY(gemm(m, m.s.act, L.down, m.s.delta, T, c.hidden, c.intermediate));
+        TRY(cs1_add_rms_norm(sc(m, s.res), sc(m, s.delta), at(m, L.post_norm), sc(m, s.x), T, c.hidden, c.eps, st));
+        TRY(gemm(m, s.x, L.gate_up, s.gate_up, T, 2 * c.intermediate, c.hidden));
+        TRY(cs1_silu_mul(sc(m, s.gate_up), 2 * c.intermediate, sc(m, s.act), T, c.intermediate, st));
+        TRY(gemm(m, s.act, L.down, s.delta, T, c.hidden, c.intermediate));
         const Tensor& next = i + 1 < m.layers.size() ? m.layers[i + 1].input_norm : m.final_norm;
-        TRY(cs1_add_rms_norm(sc(m, m.s.res), sc(m, m.s.delta), at(m, next), sc(m, m.s.x), T, c.hidden, c.eps, st));
+        TRY(cs1_add_rms_norm(sc(m, s.res), sc(m, s.delta), at(m, next), sc(m, s.x), T, c.hidden, c.eps, st));
     }
     return 0;
 }
 
-int forward(Model& m, const int32_t* ids, int T, float* last) {
-    if (T <= 0 || T > m.max_tokens || !ids || !last) return hipErrorInvalidValue;
+int embed(Model& m, const int32_t* ids, int T) {
     for (int t = 0; t < T; t++)
         if (ids[t] < 0 || ids[t] >= m.cfg.vocab) return hipErrorInvalidValue;
-    if (m.cos_len < T) TRY(rotary(m, m.max_tokens));
     TRY(cs1_upload(sc(m, m.s.ids), ids, (size_t)T * 4, m.stream));
-    TRY(cs1_embed(static_cast<const int32_t*>(sc(m, m.s.ids)), at(m, m.embed), sc(m, m.s.res), T, m.cfg.hidden,
-                  m.stream));
-    if (m.graph_enabled) {
-        auto it = m.graphs.find(T);
-        if (it != m.graphs.end()) {
-            TRY(cs1_graph_launch(it->second, m.stream));
-        } else {
-            // Run eagerly once (builds the GEMM plans and gives this call's result; run()
-            // advances the residual in place, so the captured graph is not replayed now).
-            TRY(run(m, T));
-            TRY(cs1_stream_sync(m.stream));
-            TRY(cs1_graph_begin(m.stream));
-            const int rc = run(m, T);
-            void* exec = nullptr;
-            const int rc2 = cs1_graph_end(m.stream, &exec);
-            if (rc != 0) return rc;
-            if (rc2 != 0) return rc2;
-            m.graphs[T] = exec;
-        }
-    } else {
-        TRY(run(m, T));
-    }
+    return cs1_embed(reinterpret_cast<const int32_t*>(sc(m, m.s.ids)), at(m, m.embed), sc(m, m.s.res), T,
+                     m.cfg.hidden, m.stream);
+}
+
+int forward_rows(Model& m, const int32_t* ids, int T) {
+    if (T <= 0 || T > m.max_tokens || !ids) return hipErrorInvalidValue;
+    TRY(rotary(m));
+    TRY(embed(m, ids, T));
+    if (!m.graph_enabled) return run(m, T, PLAIN, nullptr);
+    auto it = m.graphs.find(T);
+    if (it != m.graphs.end()) return cs1_graph_launch(it->second, m.stream);
+    // Run eagerly once (builds the GEMM plans and gives this call's result; run() advances
+    // the residual in place, so the captured graph is not replayed now).
+    TRY(run(m, T, PLAIN, nullptr));
+    TRY(cs1_stream_sync(m.stream));
+    TRY(cs1_graph_begin(m.stream));
+    const int rc = run(m, T, PLAIN, nullptr);
+    void* exec = nullptr;
+    const int rc2 = cs1_graph_end(m.stream, &exec);
+    if (rc != 0) return rc;
+    if (rc2 != 0) return rc2;
+    m.graphs[T] = exec;
+    return 0;
+}
+
+int forward(Model& m, const int32_t* ids, int T, float* last) {
+    if (!last) return hipErrorInvalidValue;
+    TRY(forward_rows(m, ids, T));
     std::vector<uint16_t> row(m.cfg.hidden);
-    TRY(cs1_download(row.data(), static_cast<unsigned char*>(sc(m, m.s.x)) + (size_t)(T - 1) * m.cfg.hidden * BF16,
-                     row.size() * BF16, m.stream));
+    TRY(cs1_download(row.data(), sc(m, m.s.x) + (size_t)(T - 1) * m.cfg.hidden * BF16, row.size() * BF16, m.stream));
     for (int i = 0; i < m.cfg.hidden; i++) {
         const uint32_t u = (uint32_t)row[i] << 16;
         std::memcpy(&last[i], &u, 4);
@@ -258,8 +391,94 @@ int forward(Model& m, const int32_t* ids, int T, float* last) {
     return 0;
 }
 
+// lp[r] = log softmax(lm_head h_r)[target[r]] for rows r < R of the hidden rows at `hs`.
+int token_logprobs(Model& m, size_t hs, const int32_t* targets, int R, float* lp) {
+    TRY(cs1_upload(sc(m, m.s.tgt), targets, (size_t)R * 4, m.stream));
+    TRY(gemm(m, hs, m.lm_head, m.s.logits, R, m.cfg.vocab, m.cfg.hidden));
+    logprob_kernel<<<R, 256, 0, static_cast<hipStream_t>(m.stream)>>>(
+        reinterpret_cast<const uint16_t*>(sc(m, m.s.logits)), m.cfg.vocab,
+        reinterpret_cast<const int32_t*>(sc(m, m.s.tgt)), reinterpret_cast<float*>(sc(m, m.s.lp)));
+    TRY(hipGetLastError());
+    return cs1_download(lp, sc(m, m.s.lp), (size_t)R * 4, m.stream);
+}
+
+void free_prefix(Prefix& p) {
+    if (p.mem) cs1_free(p.mem);
+    p = Prefix{};
+}
+
+int capture(Model& m, const int32_t* ids, int P) {
+    if (!ids || P < 64 || P % 64 != 0 || P > m.max_tokens) return hipErrorInvalidValue;
+    free_prefix(m.pre);
+    const Q35ModelConfig& c = m.cfg;
+    Prefix& p = m.pre;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += align256(bytes);
+        return o;
+    };
+    for (const Layer& L : m.layers) {
+        if (L.full) {
+            p.k.push_back(take((size_t)P * m.w.kv * BF16));
+            p.v.push_back(take((size_t)P * m.w.kv * BF16));
+        } else {
+            p.state.push_back(take((size_t)c.lin_v_heads * c.lin_k_dim * c.lin_v_dim * 4));
+            p.tail.push_back(take(3 * m.w.gdn_in * BF16));
+        }
+    }
+    p.last = take((size_t)c.hidden * BF16);
+    TRY(cs1_malloc(reinterpret_cast<void**>(&p.mem), off));
+    TRY(rotary(m));
+    TRY(embed(m, ids, P));
+    TRY(run(m, P, CAPTURE, nullptr));
+    TRY(cs1_copy_dd(p.mem + p.last, sc(m, m.s.x) + (size_t)(P - 1) * c.hidden * BF16, (size_t)c.hidden * BF16,
+                    m.stream));
+    TRY(cs1_stream_sync(m.stream));
+    p.len = P;
+    return 0;
+}
+
+int score(Model& m, const int32_t* ids, const int32_t* lens, int n, double* scores) {
+    if (!ids || !lens || n <= 0 || !scores || !m.cfg.lm_head || m.pre.len == 0) return hipErrorInvalidValue;
+    const int P = m.pre.len;
+    Cands cd;
+    int R = 0;
+    for (int c = 0; c < n; c++) {
+        if (lens[c] <= 0 || P + lens[c] > m.max_tokens) return hipErrorInvalidValue;
+        cd.off.push_back(R);
+        cd.len.push_back(lens[c]);
+        R += lens[c];
+        if (R > m.max_tokens) return hipErrorInvalidValue;
+    }
+    std::vector<int> pos(R);
+    for (int c = 0; c < n; c++)
+        for (int j = 0; j < lens[c]; j++) pos[cd.off[c] + j] = P + j;
+    TRY(rotary_rows(m, pos, m.s.ccos, m.s.csin));
+    TRY(embed(m, ids, R));
+    TRY(run(m, R, CANDIDATES, &cd));
+    // the row predicting token j of candidate c: the prefix's last row for j = 0, else the
+    // candidate's row j - 1
+    const size_t hb = (size_t)m.cfg.hidden * BF16;
+    for (int c = 0; c < n; c++) {
+        TRY(cs1_copy_dd(sc(m, m.s.hs) + cd.off[c] * hb, m.pre.mem + m.pre.last, hb, m.stream));
+        if (cd.len[c] > 1)
+            TRY(cs1_copy_dd(sc(m, m.s.hs) + (cd.off[c] + 1) * hb, sc(m, m.s.x) + cd.off[c] * hb, (cd.len[c] - 1) * hb,
+                            m.stream));
+    }
+    std::vector<float> lp(R);
+    TRY(token_logprobs(m, m.s.hs, ids, R, lp.data()));
+    for (int c = 0; c < n; c++) {
+        double acc = 0.0;
+        for (int j = 0; j < cd.len[c]; j++) acc += lp[cd.off[c] + j];
+        scores[c] = acc;
+    }
+    return 0;
+}
+
 void release(Model* m) {
     for (auto& kv : m->graphs) cs1_graph_destroy(kv.second);
+    free_prefix(m->pre);
     if (m->gemm) cs1_gemm_destroy(m->gemm);
     if (m->weights) cs1_free(m->weights);
     if (m->scratch) cs1_free(m->scratch);
@@ -285,7 +504,8 @@ int q35m_create(const Q35ModelConfig* cfg, uint64_t seed, int max_tokens, void**
     w.conv = 2 * w.kd + w.vd;
     w.gdn_in = w.conv + w.vd + 2 * (size_t)c.lin_v_heads;
     w.attn_q = (size_t)c.heads * c.head_dim * 2;
-    w.attn_in = w.attn_q + 2 * (size_t)c.kv_heads * c.head_dim;
+    w.kv = (size_t)c.kv_heads * c.head_dim;
+    w.attn_in = w.attn_q + 2 * w.kv;
 
     // weight arena
     size_t off = 0;
@@ -296,6 +516,7 @@ int q35m_create(const Q35ModelConfig* cfg, uint64_t seed, int max_tokens, void**
     };
     m->embed = take((size_t)c.vocab * c.hidden);
     m->final_norm = take(c.hidden);
+    if (c.lm_head) m->lm_head = take((size_t)c.vocab * c.hidden);
     m->layers.resize(c.layers);
     for (int i = 0; i < c.layers; i++) {
         Layer& L = m->layers[i];
@@ -345,12 +566,26 @@ int q35m_create(const Q35ModelConfig* cfg, uint64_t seed, int max_tokens, void**
     s.attn_in = buf(T * w.attn_in * BF16);
     s.aq = buf(T * c.heads * c.head_dim * BF16);
     s.agate = buf(T * c.heads * c.head_dim * BF16);
-    s.ak = buf(T * c.kv_heads * c.head_dim * BF16);
+    s.ak = buf(T * w.kv * BF16);
     s.ao = buf(T * c.heads * c.head_dim * BF16);
     s.gate_up = buf(T * 2 * c.intermediate * BF16);
     s.act = buf(T * c.intermediate * BF16);
     s.cos = buf(T * c.rotary_half * BF16);
     s.sin = buf(T * c.rotary_half * BF16);
+    // candidate scoring: packed rotary rows, one candidate's K/V window, its conv staging,
+    // the scored hidden rows, targets, logits and log-probabilities
+    s.ccos = buf(T * c.rotary_half * BF16);
+    s.csin = buf(T * c.rotary_half * BF16);
+    s.kwin = buf(T * w.kv * BF16);
+    s.vwin = buf(T * w.kv * BF16);
+    s.cst = buf((T + 3) * w.gdn_in * BF16);
+    s.cq = buf((T + 3) * w.kd * BF16);
+    s.ck = buf((T + 3) * w.kd * BF16);
+    s.cv = buf((T + 3) * w.vd * BF16);
+    s.hs = buf(T * c.hidden * BF16);
+    s.tgt = buf(T * 4);
+    s.logits = buf(c.lm_head ? T * c.vocab * BF16 : 0);
+    s.lp = buf(T * 4);
     s.total = off;
 
     int rc = cs1_stream_create(&m->stream);
@@ -386,6 +621,7 @@ int q35m_create(const Q35ModelConfig* cfg, uint64_t seed, int max_tokens, void**
         normal(L.gate_up);
         normal(L.down);
     }
+    if (c.lm_head) normal(m->lm_head);
     if (rc == 0) rc = cs1_stream_sync(m->stream);
     if (rc != 0) {
         release(m);
@@ -435,12 +671,31 @@ int q35m_decide(void* model, const int32_t* ids, int T, const int32_t* label_ids
     return 0;
 }
 
+int q35m_capture(void* model, const int32_t* ids, int P) {
+    if (!model) return hipErrorInvalidValue;
+    return capture(*static_cast<Model*>(model), ids, P);
+}
+
+int q35m_score(void* model, const int32_t* ids, const int32_t* lens, int n, double* scores) {
+    if (!model) return hipErrorInvalidValue;
+    return score(*static_cast<Model*>(model), ids, lens, n, scores);
+}
+
+int q35m_logprobs(void* model, const int32_t* ids, int T, float* logprobs) {
+    if (!model || !logprobs || T < 2) return hipErrorInvalidValue;
+    Model& m = *static_cast<Model*>(model);
+    if (!m.cfg.lm_head) return hipErrorInvalidValue;
+    TRY(forward_rows(m, ids, T));
+    return token_logprobs(m, m.s.x, ids + 1, T - 1, logprobs);
+}
+
 int q35m_tensor(void* model, int layer, int which, void** ptr, size_t* numel) {
     if (!model || !ptr || !numel) return hipErrorInvalidValue;
     Model& m = *static_cast<Model*>(model);
     const Tensor* t = nullptr;
     if (which == Q35M_EMBED) t = &m.embed;
     else if (which == Q35M_FINAL_NORM) t = &m.final_norm;
+    else if (which == Q35M_LM_HEAD) t = &m.lm_head;
     else {
         if (layer < 0 || layer >= (int)m.layers.size()) return hipErrorInvalidValue;
         const Layer& L = m.layers[layer];

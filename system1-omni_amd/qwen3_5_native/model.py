@@ -18,10 +18,10 @@ DEFAULT_LIB = os.path.join(os.path.dirname(_HERE), "libqwen3_5_model.so")
 EMBED, FINAL_NORM, INPUT_NORM, POST_NORM = 0, 1, 2, 3
 GDN_IN, GDN_CONV, GDN_A_LOG, GDN_DT_BIAS, GDN_NORM, GDN_OUT = 4, 5, 6, 7, 8, 9
 ATTN_QKV, ATTN_Q_NORM, ATTN_K_NORM, ATTN_O = 10, 11, 12, 13
-MLP_GATE_UP, MLP_DOWN = 14, 15
+MLP_GATE_UP, MLP_DOWN, LM_HEAD = 14, 15, 16
 
-SYMBOLS = ["q35m_create", "q35m_destroy", "q35m_set_graph", "q35m_forward", "q35m_decide", "q35m_tensor",
-           "q35m_stream"]
+SYMBOLS = ["q35m_create", "q35m_destroy", "q35m_set_graph", "q35m_forward", "q35m_decide", "q35m_capture",
+           "q35m_score", "q35m_logprobs", "q35m_tensor", "q35m_stream"]
 
 
 class _Config(ctypes.Structure):
@@ -29,7 +29,8 @@ class _Config(ctypes.Structure):
                 ("vocab", ctypes.c_int), ("heads", ctypes.c_int), ("kv_heads", ctypes.c_int),
                 ("head_dim", ctypes.c_int), ("rotary_half", ctypes.c_int), ("rope_theta", ctypes.c_double),
                 ("lin_k_heads", ctypes.c_int), ("lin_v_heads", ctypes.c_int), ("lin_k_dim", ctypes.c_int),
-                ("lin_v_dim", ctypes.c_int), ("full_attention_interval", ctypes.c_int), ("eps", ctypes.c_float)]
+                ("lin_v_dim", ctypes.c_int), ("full_attention_interval", ctypes.c_int), ("eps", ctypes.c_float),
+                ("lm_head", ctypes.c_int)]
 
 
 @dataclass(frozen=True)
@@ -49,6 +50,7 @@ class Config:
     lin_v_dim: int = 128
     full_attention_interval: int = 4
     eps: float = 1e-6
+    lm_head: int = 0
 
     def is_full(self, layer: int) -> bool:
         return (layer + 1) % self.full_attention_interval == 0
@@ -56,6 +58,11 @@ class Config:
 
 # the 4B-class hybrid decoder (32 layers, 3:1 GDN:attention).
 CFG3_4B = Config(layers=32, hidden=2560, intermediate=9728, vocab=151936, heads=16, kv_heads=4)
+# the 27B-class hybrid decoder (64 layers, 3:1), with the remaining sizes
+# (SwiGLU 17408, vocabulary 248320, untied LM head) from the reference's test config
+# tests/qwen3_5/data/config.json.
+CFG4_27B = Config(layers=64, hidden=5120, intermediate=17408, vocab=248320, heads=24, kv_heads=4, lin_k_heads=16,
+                  lin_v_heads=48, lm_head=1)
 
 _LIB = None
 
@@ -77,6 +84,9 @@ def load(path: str = None) -> ctypes.CDLL:
     lib.q35m_set_graph.argtypes = [vp, ctypes.c_int]
     lib.q35m_forward.argtypes = [vp, i32p, ctypes.c_int, f32p]
     lib.q35m_decide.argtypes = [vp, i32p, ctypes.c_int, i32p, ctypes.c_int, f32p]
+    lib.q35m_capture.argtypes = [vp, i32p, ctypes.c_int]
+    lib.q35m_score.argtypes = [vp, i32p, i32p, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    lib.q35m_logprobs.argtypes = [vp, i32p, ctypes.c_int, f32p]
     lib.q35m_tensor.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_size_t)]
     lib.q35m_stream.argtypes = [vp]
     lib.q35m_stream.restype = vp
@@ -123,6 +133,30 @@ class Model:
         hip.check(self.lib.q35m_decide(self.handle, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), len(ids),
                                        labels.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), len(labels),
                                        out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))), "q35m_decide")
+        return out
+
+    def capture(self, ids):
+        """Run a prompt prefix (length a multiple of 64) and keep its per-layer state."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        hip.check(self.lib.q35m_capture(self.handle, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), len(ids)),
+                  "q35m_capture")
+
+    def score(self, candidates) -> np.ndarray:
+        """Summed token log-probabilities of each candidate continuing the captured prefix."""
+        ids = np.ascontiguousarray(np.concatenate([np.asarray(c) for c in candidates]), np.int32)
+        lens = np.ascontiguousarray([len(c) for c in candidates], np.int32)
+        out = np.empty(len(candidates), np.float64)
+        hip.check(self.lib.q35m_score(self.handle, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                      lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), len(candidates),
+                                      out.ctypes.data_as(ctypes.POINTER(ctypes.c_double))), "q35m_score")
+        return out
+
+    def logprobs(self, ids) -> np.ndarray:
+        """log p(ids[t + 1] | ids[:t + 1]) for t < len(ids) - 1, from one full forward."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty(len(ids) - 1, np.float32)
+        hip.check(self.lib.q35m_logprobs(self.handle, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), len(ids),
+                                         out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))), "q35m_logprobs")
         return out
 
     def tensor(self, which: int, layer: int = 0) -> np.ndarray:

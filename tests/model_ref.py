@@ -17,6 +17,13 @@ def gemm(x, w, M, N, K):
 
 
 def forward(m: QM.Model, ids) -> np.ndarray:
+    """Final-norm hidden state of the last row, float."""
+    T = len(ids)
+    return O.bf16_to_f32(forward_rows(m, ids).reshape(T, m.cfg.hidden)[T - 1])
+
+
+def forward_rows(m: QM.Model, ids) -> np.ndarray:
+    """Final-norm hidden states of every row, bf16 bits [T * hidden]."""
     c = m.cfg
     T = len(ids)
     kd, vd = c.lin_k_heads * c.lin_k_dim, c.lin_v_heads * c.lin_v_dim
@@ -54,7 +61,19 @@ def forward(m: QM.Model, ids) -> np.ndarray:
         delta = gemm(act.reshape(-1), m.tensor(QM.MLP_DOWN, i), T, H, I)
         nxt = m.tensor(QM.INPUT_NORM, i + 1) if i + 1 < c.layers else m.tensor(QM.FINAL_NORM)
         res, x = O.add_rms_norm(res, delta, nxt, T, H, c.eps)
-    return O.bf16_to_f32(np.asarray(x).reshape(T, H)[T - 1])
+    return np.asarray(x).reshape(-1)
+
+
+def logprobs(m: QM.Model, ids) -> np.ndarray:
+    """log p(ids[t + 1] | ids[:t + 1]): bf16 logits from the LM head (one bf16 rounding of
+    the float64 product), then a float64 log-softmax (src/models/lfm2/engine.py:141-143 takes
+    `logits.float().log_softmax(-1)`)."""
+    T, H = len(ids), m.cfg.hidden
+    x = forward_rows(m, ids)[: (T - 1) * H]
+    logits = O.bf16_to_f32(gemm(x, m.tensor(QM.LM_HEAD), T - 1, m.cfg.vocab, H)).reshape(T - 1, -1).astype(np.float64)
+    mx = logits.max(1, keepdims=True)
+    lse = mx[:, 0] + np.log(np.exp(logits - mx).sum(1))
+    return logits[np.arange(T - 1), np.asarray(ids[1:])] - lse
 
 
 def decide(m: QM.Model, last, labels) -> np.ndarray:
