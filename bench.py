@@ -432,7 +432,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--probe", action="store_true", help="short kernel sequence for rocprofv3 counter passes")
-    ap.add_argument("--no-model", action="store_true", help="skip the config-3 decision prefill")
+    ap.add_argument("--no-model", action="store_true", help="skip the config-3 and config-4 model runs")
+    ap.add_argument("--models-only", action="store_true", help="only the config-3 and config-4 model runs")
     ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR", help="summarize rocprofv3 --pmc output of --probe")
     ap.add_argument("--summarize-trace", nargs="+", metavar="DIR", help="summarize rocprofv3 --kernel-trace output")
     args = ap.parse_args()
@@ -451,6 +452,11 @@ def main():
     st = hip.Stream()
     if args.probe:
         probe(api, st)
+        return
+    if args.models_only:
+        dec_ms, dec = bench_decision_prefill(min(args.steps, 10), args.warmup)
+        print(json.dumps({"decision_prefill_ms_4k": dec_ms, "model_cfg3": dec,
+                          "model_cfg4": bench_candidates(min(args.steps, 3), 1)}), flush=True)
         return
     ev = Events()
     attn = bench_attention(api, st, ev, args.steps, args.warmup)
