@@ -160,6 +160,16 @@ int cs1_vision_lora_add(void* x, const float* delta, size_t n, float scale, void
 int cs1_attention_ex(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse,
                      int T, int Hq, int Hk, int Dh, float scale, int q_base, void* stream);
 
+/* Varlen form of cs1_attention_ex for packed sequences (replaces the per-sequence launch
+ * loop of the reference executor, model.rs:1242-1282): cu_seqlens is a HOST array of
+ * nseq + 1 nondecreasing row offsets with cu_seqlens[0] = 0; sequence s is rows
+ * [cu_seqlens[s], cu_seqlens[s + 1]) of q, k, v (rows of ldv), gate and out, causal within
+ * itself; lse is [Hq, cu_seqlens[nseq]].  Each sequence's result equals a cs1_attention_ex
+ * call on its rows bit for bit.  One launch per 64 sequences. */
+int cs1_attention_varlen(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out,
+                         float* lse, const int32_t* cu_seqlens, int nseq, int Hq, int Hk, int Dh, float scale,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,8 @@
 //     bf16(round(o / l) * round(sigmoid(gate))) (attention.cu:221-231), optional float32
 //     log-sum-exp [Hq, T];
 //   * blocks are issued longest-first (the diagonal blocks of the causal triangle last).
+#include <type_traits>
+
 #include "common.h"
 
 namespace q35 {
@@ -218,12 +220,37 @@ __device__ unsigned long long q35_fa_ticks[8];
 // four consecutive 32-row (16 for Dh = 256) blocks of one head. Tile boundaries are fixed multiples of BN from
 // key 0 and the split is by tile parity, so a query row's arithmetic does not depend on how
 // rows are grouped into blocks (the windowed pass repeats the full pass bit for bit).
+// Packed sequences of a varlen launch (up to SEQS_MAX per launch, passed by value): sequence
+// s is rows cu[s] .. cu[s + 1] - 1 of q, k, v, gate and out, causal within itself; its
+// blocks are blockIdx.x in [blk[s], blk[s + 1]). n == 0: one sequence of T rows.
+constexpr int SEQS_MAX = 64;
+struct Seqs {
+    int n, lse_ld;
+    int cu[SEQS_MAX + 1], blk[SEQS_MAX + 1];
+};
+
 template <int D, bool GATED, bool GQA4>
 __global__ void __launch_bounds__(FA_THREADS, 1)
     flash_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int ldv,
                  const bf16* __restrict__ gate, bf16* __restrict__ out, float* __restrict__ lse, int T, int Hq, int Hk,
-                 float scale_log2, int q_base) {
+                 float scale_log2, int q_base, const Seqs seqs) {
     using Cfg = FaCfg<D>;
+    int b = blockIdx.x, lse_ld = T;
+    if (seqs.n > 0) {
+        // varlen: find this block's sequence (a scalar scan) and address it as a whole call
+        int sq = 0;
+        while (sq + 1 < seqs.n && b >= seqs.blk[sq + 1]) sq++;
+        b -= seqs.blk[sq];
+        const int r0 = seqs.cu[sq];
+        T = seqs.cu[sq + 1] - r0;
+        lse_ld = seqs.lse_ld;
+        q += (size_t)r0 * Hq * D;
+        k += (size_t)r0 * Hk * D;
+        v += (size_t)r0 * ldv;
+        if (GATED) gate += (size_t)r0 * Hq * D;
+        out += (size_t)r0 * Hq * D;
+        if (lse != nullptr) lse += r0;
+    }
     constexpr int BN = Cfg::BN, QT = (GQA4 || D == 256) ? 1 : 2;
     extern __shared__ __align__(16) unsigned char smem[];
     bf16* lds = reinterpret_cast<bf16*>(smem);
@@ -234,7 +261,6 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
     constexpr int NROWS = GQA4 ? QWW : 4 * QWW;    // query rows per block
     const int nblk = (T - q_base + NROWS - 1) / NROWS;
     const int units = GQA4 ? Hq / 4 : Hq;
-    const int b = blockIdx.x;
     const int rblk = nblk - 1 - b / units;  // longest blocks first
     const int unit = b % units;
     const int h = GQA4 ? unit * 4 + w : unit;
@@ -432,7 +458,7 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
             }
             *reinterpret_cast<u32x2*>(dst + 16 * dt) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
         }
-        if (lse != nullptr && grp == 0) lse[(size_t)h * T + qrow] = (mm + log2f(lt)) * 0.69314718055994531f;
+        if (lse != nullptr && grp == 0) lse[(size_t)h * lse_ld + qrow] = (mm + log2f(lt)) * 0.69314718055994531f;
     }
 }
 
@@ -446,10 +472,45 @@ int launch_flash(const void* q, const void* k, const void* v, int ldv, const voi
     constexpr float LOG2E = 1.4426950408889634f;
     const int nrows = GQA4 ? 16 : (D == 256 ? 64 : 128);
     const int blocks = (T - q_base + nrows - 1) / nrows * (GQA4 ? Hq / 4 : Hq);
+    Seqs one;
+    one.n = 0;
     flash_kernel<D, GATED, GQA4><<<blocks, FA_THREADS, FaCfg<D>::BYTES, st>>>(
         static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
-        static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, T, Hq, Hk, scale * LOG2E, q_base);
+        static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, T, Hq, Hk, scale * LOG2E, q_base, one);
     return hipGetLastError();
+}
+
+// Packed sequences: groups of up to SEQS_MAX sequences per launch.
+template <int D, bool GATED, bool GQA4>
+int launch_flash_varlen(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse,
+                        const int32_t* cu, int nseq, int Hq, int Hk, float scale, hipStream_t st) {
+    static const hipError_t configured = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(flash_kernel<D, GATED, GQA4>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        FaCfg<D>::BYTES);
+    if (configured != hipSuccess) return configured;
+    constexpr float LOG2E = 1.4426950408889634f;
+    const int nrows = GQA4 ? 16 : (D == 256 ? 64 : 128);
+    const int units = GQA4 ? Hq / 4 : Hq;
+    for (int s0 = 0; s0 < nseq; s0 += SEQS_MAX) {
+        Seqs sq;
+        sq.n = min(SEQS_MAX, nseq - s0);
+        sq.lse_ld = cu[nseq];
+        int blocks = 0;
+        for (int i = 0; i < sq.n; i++) {
+            sq.cu[i] = cu[s0 + i];
+            sq.blk[i] = blocks;
+            blocks += (cu[s0 + i + 1] - cu[s0 + i] + nrows - 1) / nrows * units;
+        }
+        sq.cu[sq.n] = cu[s0 + sq.n];
+        sq.blk[sq.n] = blocks;
+        if (blocks == 0) continue;
+        flash_kernel<D, GATED, GQA4><<<blocks, FA_THREADS, FaCfg<D>::BYTES, st>>>(
+            static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
+            static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, 0, Hq, Hk, scale * LOG2E, 0, sq);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 template <int D, bool GATED>
@@ -488,6 +549,33 @@ extern "C" int q35_debug_fa_ticks(unsigned long long* out) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(q35_fa_ticks), sizeof(q35_fa_ticks));
 }
 #endif
+
+extern "C" int cs1_attention_varlen(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out,
+                                    float* lse, const int32_t* cu_seqlens, int nseq, int Hq, int Hk, int Dh, float scale,
+                                    void* stream) {
+    if ((Dh != 128 && Dh != 256) || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || ldv % 8 != 0 || ldv < Hk * Dh || nseq < 0)
+        return hipErrorInvalidValue;
+    if (nseq == 0) return hipSuccess;
+    if (!cu_seqlens || cu_seqlens[0] != 0) return hipErrorInvalidValue;
+    for (int i = 0; i < nseq; i++)
+        if (cu_seqlens[i + 1] < cu_seqlens[i]) return hipErrorInvalidValue;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || (gate && !aligned16(gate)))
+        return hipErrorInvalidValue;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool g4 = (Hq / Hk) % 4 == 0;
+    auto run = [&](auto d, auto gated) {
+        constexpr int DD = decltype(d)::value;
+        constexpr bool GG = decltype(gated)::value;
+        return g4 ? launch_flash_varlen<DD, GG, true>(q, k, v, ldv, gate, out, lse, cu_seqlens, nseq, Hq, Hk, scale, st)
+                  : launch_flash_varlen<DD, GG, false>(q, k, v, ldv, gate, out, lse, cu_seqlens, nseq, Hq, Hk, scale, st);
+    };
+    using T128 = std::integral_constant<int, 128>;
+    using T256 = std::integral_constant<int, 256>;
+    using Yes = std::true_type;
+    using No = std::false_type;
+    if (Dh == 128) return gate ? run(T128{}, Yes{}) : run(T128{}, No{});
+    return gate ? run(T256{}, Yes{}) : run(T256{}, No{});
+}
 
 extern "C" int cs1_attn_prep(const void* qg, const void* kr, int ld, const void* qw, const void* kw, const void* cos,
                              const void* sin, void* q, void* gate, void* k, int T, int Hq, int Hk, int Dh, int half,

@@ -76,6 +76,7 @@ SYMBOLS = {
 # ... and this build's additions (no reference counterpart)
 ADDITIONS = {
     "cs1_attention_ex": (_I, [P, P, P, _I, P, P, P, _I, _I, _I, _I, c_float, _I, P]),
+    "cs1_attention_varlen": (_I, [P, P, P, _I, P, P, P, P, _I, _I, _I, _I, c_float, P]),
 }
 
 HIP_ERROR_INVALID_VALUE = 1

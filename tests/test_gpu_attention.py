@@ -160,3 +160,44 @@ def test_dh128_window_and_strided_v_bit_for_bit():
     emu = O.attention_emul(q, k, vv, Hk * Dh, gate, T, Hq, Hk, Dh, 0.09)
     mx, mean = bf16_errors(full, O.bf16_to_f32(emu))
     assert mx <= 2e-2 and mean <= 2e-3
+
+
+@pytest.mark.parametrize("Dh,hq,hk,gated", [(128, 16, 4, True), (128, 6, 2, False), (256, 16, 4, True),
+                                            (256, 8, 8, False)])
+def test_varlen_matches_per_sequence_calls(Dh, hq, hk, gated):
+    """cs1_attention_varlen over packed sequences equals cs1_attention_ex on each sequence's
+    rows bit for bit (outputs and LSE); 70 sequences exercise the multi-launch path."""
+    rng = np.random.default_rng(Dh + hq)
+    lens = [1, 16, 17, 64, 300, 0, 129] + list(rng.integers(1, 40, 63))
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    say(f"attention varlen Dh={Dh} {hq}/{hk} gated={gated} nseq={len(lens)} total={T}")
+    api, st = hip.api(), stream()
+    q, k, v, g = (O.f32_to_bf16(rng.standard_normal(T * h * Dh).astype(np.float32)) for h in (hq, hk, hk, hq))
+    dq, dk, dv, dg = dev(q), dev(k), dev(v), dev(g)
+    out, lse = empty(T * hq * Dh * 2), empty(hq * T * 4)
+    hip.check(api.cs1_attention_varlen(dq.at(0), dk.at(0), dv.at(0), hk * Dh, dg.at(0) if gated else None, out.at(0),
+                                       lse.at(0), cu.ctypes.data, len(lens), hq, hk, Dh, Dh ** -0.5, st.handle),
+              "varlen")
+    got = get_bf16(out, T * hq * Dh).reshape(T, hq, Dh)
+    got_lse = get(lse, np.float32, hq * T).reshape(hq, T)
+    for s in range(len(lens)):
+        a, n = int(cu[s]), int(lens[s])
+        if n == 0:
+            continue
+        sq, sk, sv, sg = (dev(x.reshape(T, -1)[a:a + n].reshape(-1)) for x in (q, k, v, g))
+        o1, l1 = empty(n * hq * Dh * 2), empty(hq * n * 4)
+        hip.check(api.cs1_attention_ex(sq.at(0), sk.at(0), sv.at(0), hk * Dh, sg.at(0) if gated else None, o1.at(0),
+                                       l1.at(0), n, hq, hk, Dh, Dh ** -0.5, 0, st.handle), "ex")
+        np.testing.assert_array_equal(got[a:a + n], get_bf16(o1, n * hq * Dh).reshape(n, hq, Dh))
+        np.testing.assert_array_equal(got_lse[:, a:a + n], get(l1, np.float32, hq * n).reshape(hq, n))
+
+
+def test_varlen_arguments():
+    api, st = hip.api(), stream()
+    say("attention varlen argument checks")
+    bad = np.array([1, 5], np.int32)
+    assert api.cs1_attention_varlen(None, None, None, 512, None, None, None, bad.ctypes.data, 1, 16, 4, 128, 0.1,
+                                    st.handle) == hip.HIP_ERROR_INVALID_VALUE
+    assert api.cs1_attention_varlen(None, None, None, 512, None, None, None, None, 0, 16, 4, 128, 0.1,
+                                    st.handle) == 0
