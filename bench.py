@@ -108,8 +108,8 @@ def timed(stream, ev, steps, warmup, launches):
     return wall_ms, per
 
 
-def bench_attention(api, st, ev, steps, warmup):
-    T, Hq, Hk, Dh = 2048, 16, 4, 128
+def bench_attention(api, st, ev, steps, warmup, T=2048):
+    Hq, Hk, Dh = 16, 4, 128
     rng = np.random.default_rng(1)
     q, k, v, gate = (hip.to_device(bf16(rng, T * h * Dh), st) for h in (Hq, Hk, Hk, Hq))
     out, lse = hip.DeviceBuffer(T * Hq * Dh * 2), hip.DeviceBuffer(Hq * T * 4)
@@ -123,7 +123,7 @@ def bench_attention(api, st, ev, steps, warmup):
     kern = per["flash_attention"]
     achieved = flops / (kern * 1e-3) / 1e12
     return {
-        "workload": "cfg1 gated GQA flash-attention prefill T=2048 Hq=16 Hk=4 Dh=128 + fp32 LSE",
+        "workload": f"cfg1 gated GQA flash-attention prefill T={T} Hq=16 Hk=4 Dh=128 + fp32 LSE",
         "tokens_per_s": T / (wall * 1e-3), "ms_per_step": wall, "kernel_ms": per,
         "roofline": {"kernel": "flash_kernel<128,gated>", "bound": "mfma", "achieved": achieved,
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,

@@ -303,9 +303,11 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
     // it + 2, then computes tile it. The barrier closing step it - 1 guarantees nobody still
     // reads that other stage, and the one closing step it publishes tile it + 1.
     TileRegs<D> regs;
+    if (ntg > 0) load_tile<D>(regs, kh, vh, ldk, ldv, grp_id * BN, T, tg);
+    // Unconditional: the compiler's wait analysis must see the Q fragments complete on every
+    // path into the loop, or it waits on the in-loop prefetches before each QK^T MFMA.
+    wait_vm_all();
     if (ntg > 0) {
-        load_tile<D>(regs, kh, vh, ldk, ldv, grp_id * BN, T, tg);
-        wait_vm_all();  // Q fragments and the first tile are in registers
         store_tile<D>(regs, gstage, tg);
         if (ntg > 1) load_tile<D>(regs, kh, vh, ldk, ldv, (2 + grp_id) * BN, T, tg);
     }
@@ -462,6 +464,373 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
     }
 }
 
+// ---------------------------------------------------------------- flash attention, Dh 128, GQA4
+//
+// flash32_kernel: the Dh = 128 GQA path (q heads per kv head a multiple of 4) on the
+// 32x32x16 MFMA (v_mfma_f32_32x32x16_bf16). A wave owns 16 query rows of two q heads (32
+// query columns), so one K or V fragment read from LDS feeds a 32x32 output tile. A block
+// owns 16 rows of the four q heads of one GQA group; its eight waves are 2 head pairs x 4 key
+// groups, group g taking the 32-key tiles g, g + 4, ... of the block's key range. Tiles move
+// from global memory straight into LDS (buffer_load_dwordx4 ... lds, no registers, no LDS
+// stores): K and V keep their row-major layout, 16-byte chunks permuted within each row so
+// fragment reads spread over the banks, and V^T fragments come out of ds_read_b64_tr_b16.
+// The four partial softmax states are merged through LDS, each key group finishing one
+// 32-dim slice of the output. Tile boundaries are fixed multiples of 32 from key 0 and the
+// merge order is fixed, so a row's arithmetic does not depend on its block (windowed and
+// packed launches repeat the full pass bit for bit).
+namespace fa32 {
+constexpr int BN = 32;                     // keys per tile
+constexpr int ROWS = 32;                   // query rows per block
+constexpr int KG = 2;                      // key groups per block
+constexpr int NSTAGE = 4;                  // LDS stages per key group
+constexpr int ROW = 256;                   // bytes per K or V row (128 bf16)
+constexpr int K_BYTES = BN * ROW;          // 8192
+constexpr int STAGE = 2 * K_BYTES;         // one K tile and one V tile
+constexpr int PART = 66;                   // floats per lane of a partial state: o (64), m, l
+constexpr int BYTES = 8 * PART * 64 * 4;   // the merge area (135168) covers 2 groups x 4 stages
+static_assert(KG * NSTAGE * STAGE <= BYTES, "stages must fit");
+// s_waitcnt with at most 8 vector memory operations outstanding (a wave issues four
+// transfers per step): vmcnt 8 (bits 3:0 = 8, bits 15:14 = 0), lgkmcnt and expcnt untouched
+constexpr int VMCNT_TWO_STEPS = 0x0f78;
+// how far (log2 units) a row's maximum may exceed the exponent base before the base moves
+constexpr float RESCALE_SLACK = 8.f;
+
+// Chunk placement, conflict-free whether the LDS serves 128 or 256 bytes per cycle: 16-byte
+// chunk c of K row r sits at slot c ^ (r & 15) (8 or 16 consecutive rows read at one chunk hit
+// distinct slots); of V row r at slot c ^ f(r & 3), f = {0, 6, 12, 10}, which separates the
+// four rows of a transposing read both within 8 slots (two adjacent chunks per row, one lane
+// group) and within 16 (four chunks per row, two lane groups).
+__device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 15); }
+__device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((0xAC60 >> (4 * (r & 3))) & 15); }
+
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+}
+
+// Buffer descriptor over rows [k0, min(T, k0 + BN)) of a row-major bf16 tensor (row stride
+// ld, rows of 128 elements); rows past T, and every row when !valid, read as zero.
+__device__ __forceinline__ u32x4 rsrc(const bf16* base, int ld, int k0, int T, bool valid) {
+    const uint64_t a = (uint64_t)(base + (size_t)k0 * ld);
+    const int rows = valid ? min(T - k0, BN) : 0;
+    const int bytes = rows > 0 ? ((rows - 1) * ld + 128) * 2 : 0;
+    // word 1: base bits 32..47, stride 0; word 3: the raw-buffer format word
+    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) & 0xffffu,
+                 (uint32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000u};
+}
+
+// One 16-byte-per-lane LDS DMA (buffer_load_dwordx4 ... lds): lane l's chunk lands at LDS
+// byte lds + 16 l. Issued as inline asm so the compiler does not treat the in-flight LDS write
+// as aliasing this step's fragment reads (it would wait for the transfer before them); the
+// kernel orders it explicitly, waiting for all transfers before the barrier that publishes
+// them. The asm is the only user of M0 in the kernel.
+__device__ __forceinline__ void dma16(const u32x4& rsrc, uint32_t lds, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(rsrc),
+                 "s"(soff)
+                 : "memory");
+}
+
+// One of a key group's four waves moves its quarter of a tile: rows 8 p .. 8 p + 7, two 1 KB
+// instructions of four rows each; lane l fills slot l % 16 of row 4 n + l / 16 with the chunk
+// that belongs there. voff[j]: per-lane byte offset within a four-row instruction (j = n for
+// K, whose permutation depends on r & 15; V's depends only on r & 3).
+__device__ __forceinline__ void dma(const u32x4& r, uint32_t dst, int ld, int p, const int* voff, bool is_k) {
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        const int row0 = 8 * p + 4 * n;
+        dma16(r, dst + row0 * ROW, voff[is_k ? n : 0], row0 * ld * 2);
+    }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 read_tr(const unsigned char* p) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                         (__attribute__((address_space(3))) s16x4*)(p)));
+}
+}  // namespace fa32
+
+template <bool GATED>
+__global__ void __launch_bounds__(512, 1)
+    flash32_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int ldv,
+                   const bf16* __restrict__ gate, bf16* __restrict__ out, float* __restrict__ lse, int T, int Hq,
+                   int Hk, float scale_log2, int q_base, const Seqs seqs) {
+    using namespace fa32;
+    constexpr int D = 128;
+    int b = blockIdx.x, lse_ld = T;
+    if (seqs.n > 0) {
+        int sq = 0;
+        while (sq + 1 < seqs.n && b >= seqs.blk[sq + 1]) sq++;
+        b -= seqs.blk[sq];
+        const int r0 = seqs.cu[sq];
+        T = seqs.cu[sq + 1] - r0;
+        lse_ld = seqs.lse_ld;
+        q += (size_t)r0 * Hq * D;
+        k += (size_t)r0 * Hk * D;
+        v += (size_t)r0 * ldv;
+        if (GATED) gate += (size_t)r0 * Hq * D;
+        out += (size_t)r0 * Hq * D;
+        if (lse != nullptr) lse += r0;
+    }
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // wave = 4 kg + 2 rh + pair: key group kg, row half rh, head pair
+    const int kg = __builtin_amdgcn_readfirstlane(wave >> 2), gw = __builtin_amdgcn_readfirstlane(wave & 3);
+    const int rh = gw >> 1, pair = gw & 1;
+    const int c32 = lane & 31, hh = lane >> 5;  // query column, lane half
+    const int units = Hq / 4;
+    const int nblk = (T - q_base + ROWS - 1) / ROWS;
+    const int unit = b % units;
+    const int q0 = q_base + (nblk - 1 - b / units) * ROWS;  // longest blocks first
+    const int hk = unit * 4 / (Hq / Hk);
+    const int h = unit * 4 + 2 * pair + (c32 >> 4);  // this lane's q head
+    const int qrow = q0 + 16 * rh + (c32 & 15);      // this lane's query row
+    const int wq0 = q0 + 16 * rh;                     // this wave's first query row
+    const bf16* kh = k + (size_t)hk * D;
+    const bf16* vh = v + (size_t)hk * D;
+    const int ldk = Hk * D;
+
+    const int kv_end = min(T, q0 + ROWS);
+    const int ntiles = (kv_end + BN - 1) / BN;
+    const int nit = (ntiles + KG - 1) / KG;                        // group 0's tiles (the most)
+    const int ntg = ntiles > kg ? (ntiles - kg + KG - 1) / KG : 0;  // this group's tiles
+    unsigned char* const gstage = smem + kg * NSTAGE * STAGE;
+    // LDS byte address of a stage (the DMA destination, a wave-uniform M0 value)
+    auto lds_addr = [&](const unsigned char* p) {
+        return (uint32_t)__builtin_amdgcn_readfirstlane(
+            (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char*)p);
+    };
+
+    // DMA lane offsets within a four-row instruction: row l / 16, slot l % 16
+    const int drow = lane >> 4, dslot = lane & 15;
+    int kvoff[2], vvoff[1];
+#pragma unroll
+    for (int j = 0; j < 2; j++) kvoff[j] = drow * ldk * 2 + (k_slot(8 * gw + 4 * j + drow, dslot) << 4);
+    vvoff[0] = drow * ldv * 2 + (v_slot(drow, dslot) << 4);
+    // the group's four waves move one tile each of K and V as eight four-row instructions
+    // tile j of the group goes to stage sidx = j % 4 (passed separately: a constant in the
+    // unrolled main loop)
+    const uint32_t gbase = lds_addr(gstage);
+    auto dma_k = [&](int j, int sidx, bool valid) {
+        dma(rsrc(kh, ldk, (kg + KG * j) * BN, T, valid), gbase + sidx * STAGE, ldk, gw, kvoff, true);
+    };
+    auto dma_v = [&](int j, int sidx, bool valid) {
+        dma(rsrc(vh, ldv, (kg + KG * j) * BN, T, valid), gbase + sidx * STAGE + K_BYTES, ldv, gw, vvoff, false);
+    };
+
+    // Pipeline prologue: K(0) and V(-1) (zeros: step 0's P V runs on an empty tile) first, the
+    // Q fragments beside them, then K(1), K(2), V(0), V(1).
+    dma_k(0, 0, ntg > 0);
+    dma_v(-1, 3, false);
+    // Q^T (B operand): column c32, dims 16 s + 8 hh .. + 7
+    u32x4 qf[8];
+    {
+        const bf16* qr = q + ((size_t)min(qrow, T - 1) * Hq + h) * D + 8 * hh;
+#pragma unroll
+        for (int s = 0; s < 8; s++) qf[s] = ldg16(qr + 16 * s);
+    }
+    // The Q fragments must be complete before the loop: an empty asm that uses them pins their
+    // loads (and the wait for them) here, so the compiler neither sinks the loads into the
+    // loop nor waits on vector memory counts there, where the transfers it does not count
+    // would turn its waits into waits for tiles in flight.
+#pragma unroll
+    for (int i = 0; i < 8; i++) asm volatile("" ::"v"(qf[i]));
+    wait_vm_all();
+    dma_k(1, 1, ntg > 1);
+    dma_v(0, 0, ntg > 0);
+    dma_k(2, 2, ntg > 2);
+    dma_v(1, 1, ntg > 1);
+    __syncthreads();
+
+    f32x16 o[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[t][i] = 0.f;
+    float m = -INFINITY, l = 0.f;
+
+    // fragment read offsets. K (A operand of S^T = K Q^T): row c32, chunk 2 ks + hh.
+    // V^T (A operand of O^T += V^T P^T) for dim tile t and k step s: lane i of lane group
+    // g = lane / 16 reads 8 bytes of row 16 s + 8 e + 4 (g / 2) + (i / 4) at dims
+    // 32 t + 16 (g % 2) + 4 (i % 4); the transposing read hands lane i the four keys of its dim.
+    const int kf = c32 * ROW;
+    const int gi = lane & 15, gg = lane >> 4;
+    const int vrow = 4 * (gg >> 1) + (gi >> 2);     // + 16 s + 8 e
+    const int vdim = 16 * (gg & 1) + 4 * (gi & 3);  // + 32 t
+    auto vt = [&](int t, int s, int e) {
+        const int r = 16 * s + 8 * e + vrow, dim = 32 * t + vdim;
+        return r * ROW + (v_slot(r, dim >> 3) << 4) + 2 * (dim & 7);
+    };
+
+    // Software pipeline, one barrier per step. Step it computes S = K Q^T of tile it on the
+    // MFMA while the VALU finishes the softmax of tile it - 1 and then issues its P V, so a
+    // wave always has independent MFMA work in flight. Stage j % 4 holds K(j) and V(j); step it
+    // issues K(it + 3) and V(it + 2) into the stage whose K (it - 1) and V (it - 2) the barrier
+    // closing step it - 1 released, and before its own barrier waits for the transfers of step
+    // it - 2 (K(it + 1), V(it)), which step it + 1 reads: two steps of transfers stay in flight.
+    // Transfers are unconditional: tiles past the group's range read as zero and land in slots
+    // nobody reads. Every step runs the same code: a tile past the group's range (or the
+    // "previous tile" of step 0, whose scores start at -inf) lies beyond every query row of the
+    // wave, so the causal mask sends all its scores to -inf and it adds exact zeros.
+    //
+    // The exponent base m moves lazily: only when some row's maximum exceeds it by more than
+    // RESCALE_SLACK (log2 units), so a probability is at most 2^RESCALE_SLACK and O and l are
+    // rescaled a few times per row instead of at nearly every step.
+    f32x16 s;  // scores of the tile whose softmax is pending
+#pragma unroll
+    for (int i = 0; i < 16; i++) s[i] = -INFINITY;
+    // sc = it % 4; may_mask: tile it - 1 can reach the diagonal or T (the general loop)
+    auto step = [&](int it, int sc, bool may_mask) {
+        dma_k(it + 3, (sc + 3) & 3, it + 3 < ntg);
+        dma_v(it + 2, (sc + 2) & 3, it + 2 < ntg);
+        // softmax statistics of tile it - 1: s[i] is key k0 + 8 (i / 4) + 4 hh + i % 4
+        const int k0 = (kg + KG * (it - 1)) * BN;
+        if (may_mask && (k0 + BN - 1 > wq0 || k0 + BN > T)) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int key = k0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+                if (key > qrow || key >= T) s[i] = -INFINITY;
+            }
+        }
+        float mx = s[0];
+#pragma unroll
+        for (int i = 1; i < 16; i++) mx = fmaxf(mx, s[i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+        if (!__all(mx <= m + RESCALE_SLACK)) {
+            const float mn = fmaxf(m, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
+            m = mn;
+            l *= alpha;
+#pragma unroll
+            for (int t = 0; t < 4; t++) o[t] *= alpha;
+        }
+        const float base = m == -INFINITY ? 0.f : m;
+        // one basic block: all of the step's fragments read from LDS first (one exposed LDS
+        // latency per step), then QK^T of tile it on the MFMA beside the exponentials of tile
+        // it - 1, then O^T += V^T P^T of tile it - 1
+        const unsigned char* kb = gstage + sc * STAGE;
+        const unsigned char* vb = gstage + ((sc + 3) & 3) * STAGE + K_BYTES;
+        u32x4 kfr[8], vfr[4][2];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            kfr[ks] = *reinterpret_cast<const u32x4*>(kb + kf + (k_slot(c32, 2 * ks + hh) << 4));
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const u32x2 lo = read_tr(vb + vt(t, j, 0)), hi = read_tr(vb + vt(t, j, 1));
+                vfr[t][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            }
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs that consume them
+        f32x16 sn;
+#pragma unroll
+        for (int i = 0; i < 16; i++) sn[i] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) sn = mfma32(kfr[ks], qf[ks], sn);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            s[i] = __builtin_amdgcn_exp2f(fmaf(s[i], scale_log2, -base));
+            l += s[i];
+        }
+        // P^T (B operand) of k step j: k index 8 hh + e is key 16 j + 4 hh + e (e < 4) or
+        // 16 j + 8 + 4 hh + e - 4, i.e. s[8 j + e]
+        u32x4 pf[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            pf[j] = u32x4{pack2(s[8 * j], s[8 * j + 1]), pack2(s[8 * j + 2], s[8 * j + 3]),
+                          pack2(s[8 * j + 4], s[8 * j + 5]), pack2(s[8 * j + 6], s[8 * j + 7])};
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) o[t] = mfma32(vfr[t][j], pf[j], o[t]);
+        s = sn;
+        // the transfers of step it - 2 (issued before this step's four) have landed
+        __builtin_amdgcn_s_waitcnt(VMCNT_TWO_STEPS);
+        __syncthreads();
+    };
+    // Steps 0 .. n_main - 1 see no masked tile: step 0's previous tile is the empty one, and
+    // the group's tiles kg + 2 m with 32 (kg + 2 m) <= lim lie wholly below this wave's first
+    // row and below T; the remaining steps (diagonal, tail, past the range) run the general
+    // loop with the mask.
+    const int lim = min(wq0 + 1, T) - BN;
+    const int ulast = lim >= 0 ? lim / BN : -1;  // last unmasked tile index
+    const int n_main = ulast >= kg ? (ulast - kg) / KG + 2 : 1;
+    int it = 0;
+    for (; it < n_main; it++) step(it, it & 3, false);
+    for (; it <= nit; it++) step(it, it & 3, true);
+    wait_vm_all();  // trailing transfers (all zero-length) land before the stages are reused
+    __syncthreads();
+
+    // o[t][i]: dim 32 t + 8 (i / 4) + 4 hh + i % 4 of query column c32. Key group kg finishes
+    // dims [64 kg, 64 kg + 64) of its rows and head pair from the two groups' partial states.
+    u32x2 gp[8];
+    const size_t orow = ((size_t)min(qrow, T - 1) * Hq + h) * D + 64 * kg + 4 * hh;
+    if (GATED) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) gp[j] = *reinterpret_cast<const u32x2*>(gate + orow + 8 * j);
+    }
+    float* part = reinterpret_cast<float*>(smem);
+    {
+        float* pp = part + wave * PART * 64 + lane;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) pp[(16 * t + i) * 64] = o[t][i];
+        pp[64 * 64] = m;
+        pp[65 * 64] = l;
+    }
+    __syncthreads();
+    float mk[KG], ak[KG];
+    float mm = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < KG; g++) {
+        mk[g] = part[((4 * g + gw) * PART + 64) * 64 + lane];
+        mm = fmaxf(mm, mk[g]);
+    }
+    const float base = mm == -INFINITY ? 0.f : mm;
+    float lt = 0.f;
+#pragma unroll
+    for (int g = 0; g < KG; g++) {
+        ak[g] = __builtin_amdgcn_exp2f(mk[g] - base);
+        lt += part[((4 * g + gw) * PART + 65) * 64 + lane] * ak[g];
+    }
+    lt += __shfl_xor(lt, 32, 64);
+    if (qrow >= T) return;
+    const float inv = 1.f / lt;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float a[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int g = 0; g < KG; g++) acc += part[((4 * g + gw) * PART + 32 * kg + 4 * j + r) * 64 + lane] * ak[g];
+            a[r] = acc * inv;
+        }
+        if (GATED) {
+            a[0] = round_bf16(a[0]) * round_bf16(sigmoid(lo_f32(gp[j][0])));
+            a[1] = round_bf16(a[1]) * round_bf16(sigmoid(hi_f32(gp[j][0])));
+            a[2] = round_bf16(a[2]) * round_bf16(sigmoid(lo_f32(gp[j][1])));
+            a[3] = round_bf16(a[3]) * round_bf16(sigmoid(hi_f32(gp[j][1])));
+        }
+        *reinterpret_cast<u32x2*>(out + orow + 8 * j) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
+    }
+    if (lse != nullptr && kg == 0 && hh == 0) lse[(size_t)h * lse_ld + qrow] = (mm + log2f(lt)) * 0.69314718055994531f;
+}
+
+template <bool GATED>
+int launch_flash32(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse, int T,
+                   int Hq, int Hk, float scale, int q_base, int blocks, const Seqs& sq, hipStream_t st) {
+    static const hipError_t configured = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(flash32_kernel<GATED>), hipFuncAttributeMaxDynamicSharedMemorySize, fa32::BYTES);
+    if (configured != hipSuccess) return configured;
+    flash32_kernel<GATED><<<blocks, 512, fa32::BYTES, st>>>(
+        static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
+        static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, T, Hq, Hk, scale * 1.4426950408889634f, q_base,
+        sq);
+    return hipGetLastError();
+}
+
 template <int D, bool GATED, bool GQA4>
 int launch_flash(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse, int T,
                  int Hq, int Hk, float scale, int q_base, hipStream_t st) {
@@ -474,6 +843,9 @@ int launch_flash(const void* q, const void* k, const void* v, int ldv, const voi
     const int blocks = (T - q_base + nrows - 1) / nrows * (GQA4 ? Hq / 4 : Hq);
     Seqs one;
     one.n = 0;
+    if (D == 128 && GQA4)
+        return launch_flash32<GATED>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base,
+                                     (T - q_base + fa32::ROWS - 1) / fa32::ROWS * (Hq / 4), one, st);
     flash_kernel<D, GATED, GQA4><<<blocks, FA_THREADS, FaCfg<D>::BYTES, st>>>(
         static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
         static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, T, Hq, Hk, scale * LOG2E, q_base, one);
@@ -489,7 +861,7 @@ int launch_flash_varlen(const void* q, const void* k, const void* v, int ldv, co
         FaCfg<D>::BYTES);
     if (configured != hipSuccess) return configured;
     constexpr float LOG2E = 1.4426950408889634f;
-    const int nrows = GQA4 ? 16 : (D == 256 ? 64 : 128);
+    const int nrows = (D == 128 && GQA4) ? fa32::ROWS : GQA4 ? 16 : (D == 256 ? 64 : 128);
     const int units = GQA4 ? Hq / 4 : Hq;
     for (int s0 = 0; s0 < nseq; s0 += SEQS_MAX) {
         Seqs sq;
@@ -504,6 +876,11 @@ int launch_flash_varlen(const void* q, const void* k, const void* v, int ldv, co
         sq.cu[sq.n] = cu[s0 + sq.n];
         sq.blk[sq.n] = blocks;
         if (blocks == 0) continue;
+        if (D == 128 && GQA4) {
+            const int e = launch_flash32<GATED>(q, k, v, ldv, gate, out, lse, 0, Hq, Hk, scale, 0, blocks, sq, st);
+            if (e != hipSuccess) return e;
+            continue;
+        }
         flash_kernel<D, GATED, GQA4><<<blocks, FA_THREADS, FaCfg<D>::BYTES, st>>>(
             static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
             static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, 0, Hq, Hk, scale * LOG2E, 0, sq);
