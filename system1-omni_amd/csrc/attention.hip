@@ -543,6 +543,12 @@ __device__ __forceinline__ void dma(const u32x4& r, uint32_t dst, int ld, int p,
     }
 }
 
+// Maximum over the two lane halves (lanes l and l ^ 32): one v_permlane32_swap, no LDS trip.
+__device__ __forceinline__ float max_halves(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x2 read_tr(const unsigned char* p) {
     return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -681,8 +687,21 @@ __global__ void __launch_bounds__(512, 1)
     for (int i = 0; i < 16; i++) s[i] = -INFINITY;
     // sc = it % 4; may_mask: tile it - 1 can reach the diagonal or T (the general loop)
     auto step = [&](int it, int sc, bool may_mask) {
+        // Issue order within a step (all eight waves start it together after the barrier):
+        // the K fragment reads, the K(it + 3) transfer, the softmax statistics of tile it - 1
+        // while those reads are in flight, the V fragment reads, QK^T of tile it beside the
+        // exponentials, the V(it + 2) transfer, then P V. Spreading the two transfers through
+        // the step keeps a wave from stalling on a full memory queue when every wave issues at
+        // once.
+        const unsigned char* kb = gstage + sc * STAGE;
+        const unsigned char* vb = gstage + ((sc + 3) & 3) * STAGE + K_BYTES;
+        u32x4 kfr[8], vfr[4][2];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            kfr[ks] = *reinterpret_cast<const u32x4*>(kb + kf + (k_slot(c32, 2 * ks + hh) << 4));
+        __builtin_amdgcn_sched_barrier(0);
         dma_k(it + 3, (sc + 3) & 3, it + 3 < ntg);
-        dma_v(it + 2, (sc + 2) & 3, it + 2 < ntg);
+        __builtin_amdgcn_sched_barrier(0);
         // softmax statistics of tile it - 1: s[i] is key k0 + 8 (i / 4) + 4 hh + i % 4
         const int k0 = (kg + KG * (it - 1)) * BN;
         if (may_mask && (k0 + BN - 1 > wq0 || k0 + BN > T)) {
@@ -695,7 +714,7 @@ __global__ void __launch_bounds__(512, 1)
         float mx = s[0];
 #pragma unroll
         for (int i = 1; i < 16; i++) mx = fmaxf(mx, s[i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+        mx = max_halves(mx) * scale_log2;
         if (!__all(mx <= m + RESCALE_SLACK)) {
             const float mn = fmaxf(m, mx);
             const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
@@ -705,15 +724,6 @@ __global__ void __launch_bounds__(512, 1)
             for (int t = 0; t < 4; t++) o[t] *= alpha;
         }
         const float base = m == -INFINITY ? 0.f : m;
-        // one basic block: all of the step's fragments read from LDS first (one exposed LDS
-        // latency per step), then QK^T of tile it on the MFMA beside the exponentials of tile
-        // it - 1, then O^T += V^T P^T of tile it - 1
-        const unsigned char* kb = gstage + sc * STAGE;
-        const unsigned char* vb = gstage + ((sc + 3) & 3) * STAGE + K_BYTES;
-        u32x4 kfr[8], vfr[4][2];
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++)
-            kfr[ks] = *reinterpret_cast<const u32x4*>(kb + kf + (k_slot(c32, 2 * ks + hh) << 4));
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -721,7 +731,8 @@ __global__ void __launch_bounds__(512, 1)
                 const u32x2 lo = read_tr(vb + vt(t, j, 0)), hi = read_tr(vb + vt(t, j, 1));
                 vfr[t][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
             }
-        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs that consume them
+        __builtin_amdgcn_sched_barrier(0);
+        // QK^T of tile it on the MFMA beside the exponentials of tile it - 1
         f32x16 sn;
 #pragma unroll
         for (int i = 0; i < 16; i++) sn[i] = 0.f;
@@ -739,6 +750,9 @@ __global__ void __launch_bounds__(512, 1)
         for (int j = 0; j < 2; j++)
             pf[j] = u32x4{pack2(s[8 * j], s[8 * j + 1]), pack2(s[8 * j + 2], s[8 * j + 3]),
                           pack2(s[8 * j + 4], s[8 * j + 5]), pack2(s[8 * j + 6], s[8 * j + 7])};
+        __builtin_amdgcn_sched_barrier(0);
+        dma_v(it + 2, (sc + 2) & 3, it + 2 < ntg);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
