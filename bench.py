@@ -125,7 +125,7 @@ def bench_attention(api, st, ev, steps, warmup, T=2048):
     return {
         "workload": f"cfg1 gated GQA flash-attention prefill T={T} Hq=16 Hk=4 Dh=128 + fp32 LSE",
         "tokens_per_s": T / (wall * 1e-3), "ms_per_step": wall, "kernel_ms": per,
-        "roofline": {"kernel": "flash_kernel<128,gated>", "bound": "mfma", "achieved": achieved,
+        "roofline": {"kernel": "flash32_kernel<gated>", "bound": "mfma", "achieved": achieved,
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
                      "algorithmic_flop": flops},
     }
@@ -340,6 +340,7 @@ def probe(api, st):
     FETCH_SIZE / WRITE_SIZE counters (it reads and writes exactly that many bytes)."""
     ev = Events()
     bench_attention(api, st, ev, 3, 0)
+    bench_attention(api, st, ev, 3, 0, T=8192)
     bench_gdn(api, st, ev, 3, 0, 8192, 32, 16, True, 0.01, 2, "cfg2")
     bench_gdn(api, st, ev, 3, 0, 512, 16, 16, False, 0.0, 0, "cfg0")
     bench_hbm_ops(api, st, ev, 3, 0)
@@ -460,6 +461,7 @@ def main():
         return
     ev = Events()
     attn = bench_attention(api, st, ev, args.steps, args.warmup)
+    attn8k = bench_attention(api, st, ev, max(2, args.steps // 4), 1, T=8192)
     g2 = bench_gdn(api, st, ev, args.steps, args.warmup, 8192, 32, 16, True, 0.01, 2,
                    "cfg2 conv1d(k=4)+SiLU then GDN chunked prefill T=8192 HK=16 H=32 D=128, S0~N(0,0.01)")
     g0 = bench_gdn(api, st, ev, args.steps, args.warmup, 512, 16, 16, False, 0.0, 0,
@@ -475,9 +477,9 @@ def main():
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs of the BASELINE shapes)",
         "config": {"workload": attn["workload"], "global_batch": 1, "seq_len": 2048, "parallelism": "none"},
         "roofline": {k: attn["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac")} |
-                    {"traffic": traffic_bytes("q35::(anonymous namespace)::flash_kernel<128, true, true>")},
+                    {"traffic": traffic_bytes("q35::(anonymous namespace)::flash32_kernel<true> grid=131072 ")},
         "cpu_baseline": cpu,
-        "layers": {"attention_cfg1": attn, "gdn_cfg2": g2, "gdn_cfg0": g0},
+        "layers": {"attention_cfg1": attn, "attention_t8192": attn8k, "gdn_cfg2": g2, "gdn_cfg0": g0},
         "hbm_ops": hbm,
         "decision_prefill_ms_4k": dec_ms,
         "model_cfg3": dec,
