@@ -32,7 +32,7 @@
 //         scan's MFMA consumes it (1 KB per wave per store, fully coalesced).
 //   * gdn_scan, grid (head x 8 slices of 16 value columns), 4 waves.  The float32 state
 //     slice 128 x 16 lives in MFMA accumulators; each chunk streams its operand
-//     fragments from HBM/L2 straight into registers (two chunks ahead) and exchanges only
+//     fragments from HBM/L2 straight into registers (three chunks ahead) and exchanges only
 //     bf16(S) and v_new through LDS.  The output o = qd Sb + pb v_new is produced in the
 //     same pass, so per-chunk states and v_new never go to memory.  The slices of one head
 //     run on the same XCD (block = slice * H + head) and share its L2.
@@ -570,9 +570,13 @@ __global__ void __launch_bounds__(ST)
             Q35_LPHASE(8);
             __syncthreads();  // A
             Q35_LPHASE(9);
+            u32x4 sb[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) sb[s] = lds_perm(sbt, SLD, col, s, grp);
+            __builtin_amdgcn_sched_barrier(0);  // all four reads in flight before the first MFMA
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 4; s++) acc = mfma16(cur.w[s], lds_perm(sbt, SLD, col, s, grp), acc);
+            for (int s = 0; s < 4; s++) acc = mfma16(cur.w[s], sb[s], acc);
             const float vn0 = lo_f32(cur.u[0]) - acc[0], vn1 = hi_f32(cur.u[0]) - acc[1];
             const float vn2 = lo_f32(cur.u[1]) - acc[2], vn3 = hi_f32(cur.u[1]) - acc[3];
             *reinterpret_cast<u32x2*>(vnt + col * VLD + 16 * rb + 4 * grp) = u32x2{pack2(vn0, vn1), pack2(vn2, vn3)};
@@ -580,6 +584,7 @@ __global__ void __launch_bounds__(ST)
             __syncthreads();  // B
             Q35_LPHASE(11);
             const u32x4 vb0 = lds_perm(vnt, VLD, col, 0, grp), vb1 = lds_perm(vnt, VLD, col, 1, grp);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 st[i] *= cur.decay;
@@ -588,18 +593,23 @@ __global__ void __launch_bounds__(ST)
             }
             Q35_LPHASE(12);
         };
-        ChainOps opa, opb, opc;
+        // four rotating operand sets: chunk c + 3 is requested while chunk c is processed
+        ChainOps opa, opb, opc, opd;
         load_chain(opa, sr, decay, at(0), rb, lane, slice);
         load_chain(opb, sr, decay, at(1), rb, lane, slice);
-        for (int c = 0; c < NC; c += 3) {
-            load_chain(opc, sr, decay, at(c + 2), rb, lane, slice);
+        load_chain(opc, sr, decay, at(2), rb, lane, slice);
+        for (int c = 0; c < NC; c += 4) {
+            load_chain(opd, sr, decay, at(c + 3), rb, lane, slice);
             step(opa);
             if (c + 1 >= NC) break;
-            load_chain(opa, sr, decay, at(c + 3), rb, lane, slice);
+            load_chain(opa, sr, decay, at(c + 4), rb, lane, slice);
             step(opb);
             if (c + 2 >= NC) break;
-            load_chain(opb, sr, decay, at(c + 4), rb, lane, slice);
+            load_chain(opb, sr, decay, at(c + 5), rb, lane, slice);
             step(opc);
+            if (c + 3 >= NC) break;
+            load_chain(opc, sr, decay, at(c + 6), rb, lane, slice);
+            step(opd);
         }
         Q35_LPHASE_FLUSH();
         if (s_out) {
@@ -612,30 +622,40 @@ __global__ void __launch_bounds__(ST)
     } else {
         auto step = [&](const OutOps& cur, int c) {
             __syncthreads();  // A
+            u32x4 sb[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) sb[s] = lds_perm(sbt, SLD, col, s, grp);
+            __builtin_amdgcn_sched_barrier(0);
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 4; s++) acc = mfma16(cur.qd[s], lds_perm(sbt, SLD, col, s, grp), acc);
+            for (int s = 0; s < 4; s++) acc = mfma16(cur.qd[s], sb[s], acc);
             __syncthreads();  // B
-#pragma unroll
-            for (int s = 0; s < 2; s++) acc = mfma16(cur.pb[s], lds_perm(vnt, VLD, col, s, grp), acc);
+            const u32x4 vb0 = lds_perm(vnt, VLD, col, 0, grp), vb1 = lds_perm(vnt, VLD, col, 1, grp);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = mfma16(cur.pb[0], vb0, acc);
+            acc = mfma16(cur.pb[1], vb1, acc);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int t = c * C + 16 * rb + 4 * grp + r;
                 if (t < T) o[((size_t)t * H + h) * DK + v0 + col] = to_bf16(acc[r]);
             }
         };
-        OutOps opa, opb, opc;
+        OutOps opa, opb, opc, opd;
         load_out(opa, sr, at(0), rb, lane);
         load_out(opb, sr, at(1), rb, lane);
-        for (int c = 0; c < NC; c += 3) {
-            load_out(opc, sr, at(c + 2), rb, lane);
+        load_out(opc, sr, at(2), rb, lane);
+        for (int c = 0; c < NC; c += 4) {
+            load_out(opd, sr, at(c + 3), rb, lane);
             step(opa, c);
             if (c + 1 >= NC) break;
-            load_out(opa, sr, at(c + 3), rb, lane);
+            load_out(opa, sr, at(c + 4), rb, lane);
             step(opb, c + 1);
             if (c + 2 >= NC) break;
-            load_out(opb, sr, at(c + 4), rb, lane);
+            load_out(opb, sr, at(c + 5), rb, lane);
             step(opc, c + 2);
+            if (c + 3 >= NC) break;
+            load_out(opc, sr, at(c + 6), rb, lane);
+            step(opd, c + 3);
         }
     }
 }
