@@ -145,6 +145,20 @@ def test_config1_dh128_gated_with_lse(T):
     assert worst < 1.6e-2
 
 
+@pytest.mark.parametrize("hq,hk", [(32, 4), (8, 1), (12, 3)])
+def test_dh128_head_ratios_vs_emulator(hq, hk):
+    """GQA ratios beyond 4 q heads per kv head and odd kv-head counts on the Dh=128 path."""
+    T, Dh = 257, 128
+    say(f"attention Dh=128 hq={hq} hk={hk} T={T}")
+    q, k, v, gate = cfg1_inputs(T, hq, hk, Dh, seed=5)
+    out, lse = attn(dev(q), dev(k), dev(v), hk * Dh, dev(gate), T, hq, hk, Dh, Dh ** -0.5, lse=True)
+    emu, else_ = O.attention_emul(q, k, v, hk * Dh, gate, T, hq, hk, Dh, Dh ** -0.5, want_lse=True)
+    mx, mean = bf16_errors(out, O.bf16_to_f32(emu))
+    say(f"  vs emulated reference kernel: max-abs {mx:.2e} mean-abs {mean:.2e}")
+    assert mx <= 2e-2 and mean <= 2e-3
+    np.testing.assert_allclose(lse, else_, atol=1e-3, rtol=0)
+
+
 def test_dh128_window_and_strided_v_bit_for_bit():
     T, Hq, Hk, Dh = 700, 8, 2, 128
     q, k, _, gate = cfg1_inputs(T, Hq, Hk, Dh, seed=3)
