@@ -170,6 +170,20 @@ int cs1_attention_varlen(const void* q, const void* k, const void* v, int ldv, c
                          float* lse, const int32_t* cu_seqlens, int nseq, int Hq, int Hk, int Dh, float scale,
                          void* stream);
 
+/* Varlen form of cs1_gdn_prefill_x for packed sequences (the candidate-packed prefill of the
+ * reference's scoring path, model.rs:1421-1470, which runs the delta rule per candidate):
+ * cu_seqlens is a HOST array of nseq + 1 (at most 64) nondecreasing row offsets with
+ * cu_seqlens[0] = 0; sequence s is rows [cu_seqlens[s], cu_seqlens[s + 1]) of q, k (rows of
+ * HK * 128), v and o (rows of H * 128), g and beta (rows of H).  Sequence s starts from the
+ * float32 state s_in + s * s_in_stride ([H, 128, 128]; stride 0: one state shared by all,
+ * s_in null: zeros) and, when s_out is non-null, leaves its final state at
+ * s_out + s * s_out_stride.  Chunks restart at each sequence (each result equals a
+ * cs1_gdn_prefill_x call on the sequence's rows bit for bit).  The workspace must hold
+ * cs1_gdn_workspace_floats(64 * sum_s ceil(len_s / 64), H) floats.  One launch pair. */
+int cs1_gdn_prefill_varlen(const void* q, const void* k, const void* v, const float* g, const void* beta, void* o,
+                           float* workspace, const int32_t* cu_seqlens, int nseq, int H, int HK, float scale,
+                           const void* s_in, size_t s_in_stride, void* s_out, size_t s_out_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

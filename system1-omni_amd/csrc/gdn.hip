@@ -68,8 +68,9 @@ constexpr size_t FRAG = 64;  // lanes per fragment (u32x4 or u32x2 each)
 
 struct Layout {
     size_t w, qd, kd, pb, u, decay, total;
-    Layout(int T, int H) {
-        const size_t NC = (size_t)((T + C - 1) / C), n = (size_t)H * NC;
+    // NC chunks (records per head)
+    Layout(size_t NC, int H) {
+        const size_t n = (size_t)H * NC;
         size_t at = 0;
         auto take = [&](size_t bytes) {
             const size_t off = at;
@@ -86,8 +87,16 @@ struct Layout {
     }
 };
 
-Work split(float* workspace, int T, int H) {
-    const Layout l(T, H);
+// packed sequences of one launch (up to GSEQS_MAX): sequence s is token rows tok[s] ..
+// tok[s + 1] - 1 and workspace chunks chk[s] .. chk[s + 1] - 1; n == 0: one sequence
+constexpr int GSEQS_MAX = 64;
+struct GSeqs {
+    int n;
+    int tok[GSEQS_MAX + 1], chk[GSEQS_MAX + 1];
+};
+
+Work split(float* workspace, size_t NC, int H) {
+    const Layout l(NC, H);
     unsigned char* b = reinterpret_cast<unsigned char*>(workspace);
     return Work{reinterpret_cast<u32x4*>(b + l.w),  reinterpret_cast<u32x4*>(b + l.qd),
                 reinterpret_cast<u32x4*>(b + l.kd), reinterpret_cast<u32x4*>(b + l.pb),
@@ -136,6 +145,8 @@ __device__ __forceinline__ u32x4 select_op(int half, int col, int grp) {
     }
     return u32x4{v[0], v[1], v[2], v[3]};
 }
+
+__device__ __forceinline__ int tid_of_block() { return threadIdx.x; }
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -191,7 +202,8 @@ __device__ unsigned long long q35_phase_ticks[16];
 
 __global__ void __launch_bounds__(PT)
     gdn_prep(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-             const float* __restrict__ g, const bf16* __restrict__ beta, Work ws, int T, int H, int HK, float scale) {
+             const float* __restrict__ g, const bf16* __restrict__ beta, Work ws, int T, int H, int HK, float scale,
+             const GSeqs gs) {
     extern __shared__ __align__(16) unsigned char sm[];
     u32x4* khi_pl = reinterpret_cast<u32x4*>(sm + R0);
     u32x4* klo_pl = reinterpret_cast<u32x4*>(sm + R0 + PLANE);
@@ -205,11 +217,25 @@ __global__ void __launch_bounds__(PT)
     float* kinv_s = erem + C;
 
     const int c = blockIdx.x, h = blockIdx.y, NC = gridDim.x;
+    int cl = c;  // chunk within its sequence
+    if (gs.n > 0) {
+        // packed sequences: find this chunk's sequence (a scalar scan) and address it alone
+        int sq = 0;
+        while (sq + 1 < gs.n && c >= gs.chk[sq + 1]) sq++;
+        cl = c - gs.chk[sq];
+        const int r0 = gs.tok[sq];
+        T = gs.tok[sq + 1] - r0;
+        q += (size_t)r0 * HK * DK;
+        k += (size_t)r0 * HK * DK;
+        v += (size_t)r0 * H * DK;
+        g += (size_t)r0 * H;
+        beta += (size_t)r0 * H;
+    }
     const int hk = h / (H / HK);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
     float* scr = reinterpret_cast<float*>(sm + R0_SC) + wave * 256;
     const size_t rec = (size_t)h * NC + c;
-    const int t0 = c * C;
+    const int t0 = cl * C;
     Q35_PHASE_START();
 
     // 0. loads: own k rows (block `wave`), q rows (block 3 - wave), and the k and v columns
@@ -538,15 +564,37 @@ __device__ __forceinline__ u32x4 lds_perm(const bf16* base, int ld, int col, int
 // before the next A, when v_new is rewritten.
 __global__ void __launch_bounds__(ST)
     gdn_scan(Work ws, const float* __restrict__ decay_all, bf16* __restrict__ o, int T, int H, int NC,
-             const float* __restrict__ s_in, float* __restrict__ s_out) {
+             const float* __restrict__ s_in, size_t s_in_stride, float* __restrict__ s_out, size_t s_out_stride,
+             const GSeqs gs) {
     __shared__ __align__(16) bf16 sbt[BV * SLD];
     __shared__ __align__(16) bf16 vnt[BV * VLD];
-    const int h = blockIdx.x % H, slice = blockIdx.x / H, v0 = slice * BV;
+    const int h = blockIdx.x % H, slice = (blockIdx.x / H) % NS, v0 = slice * BV;
+    size_t rec0 = (size_t)h * NC;
+    if (gs.n > 0) {
+        // packed sequences: blocks (sequence, slice, head); each sequence is scanned alone
+        // from its own (or the shared) initial state over its own chunks
+        const int sq = blockIdx.x / (H * NS);
+        rec0 += gs.chk[sq];
+        NC = gs.chk[sq + 1] - gs.chk[sq];
+        T = gs.tok[sq + 1] - gs.tok[sq];
+        o += (size_t)gs.tok[sq] * H * DK;
+        if (s_in) s_in += sq * s_in_stride;
+        if (s_out) s_out += sq * s_out_stride;
+        if (NC == 0) {
+            // an empty sequence: its final state is its initial state (the whole block leaves
+            // here, before any barrier)
+            if (s_out != nullptr && tid_of_block() < 128)
+                for (int x = tid_of_block(); x < DK * BV; x += 128) {
+                    const size_t at_ = ((size_t)h * DK + x / BV) * DK + v0 + x % BV;
+                    s_out[at_] = s_in ? s_in[at_] : 0.f;
+                }
+            return;
+        }
+    }
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
     const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform for the compiler
     const bool chain = uwave < 4;
     const int rb = uwave & 3;  // row block: state rows 32 rb .. (chain) / output rows 16 rb .. (output)
-    const size_t rec0 = (size_t)h * NC;
     auto at = [&](int c) { return min(c, NC - 1); };
     const Streams sr{stream_rsrc(ws.w + rec0 * 16 * FRAG), stream_rsrc(ws.kd + rec0 * 16 * FRAG),
                      stream_rsrc(ws.qd + rec0 * 16 * FRAG), stream_rsrc(ws.pb + rec0 * 8 * FRAG),
@@ -667,13 +715,16 @@ __global__ void __launch_bounds__(256) state_pass(const float4* __restrict__ s_i
     if (i < n4) s_out[i] = s_in ? s_in[i] : float4{0.f, 0.f, 0.f, 0.f};
 }
 
+// One launch over packed sequences: gs.n == 0 is a single sequence of T rows; otherwise T is
+// the total row count and gs describes the sequences (their chunk offsets filled here).
 int gdn_run(const void* q, const void* k, const void* v, const float* g, const void* beta, void* o, float* workspace,
-            int T, int H, int HK, float scale, const void* s_in, void* s_out, void* stream) {
+            int T, int H, int HK, float scale, const void* s_in, size_t s_in_stride, void* s_out,
+            size_t s_out_stride, GSeqs gs, void* stream) {
     if (T < 0 || H <= 0 || HK <= 0 || H % HK != 0) return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const float* si = static_cast<const float*>(s_in);
     float* so = static_cast<float*>(s_out);
-    if (T == 0) {
+    if (gs.n == 0 && T == 0) {
         if (so == nullptr) return hipSuccess;
         const size_t n4 = (size_t)H * DK * DK / 4;
         state_pass<<<cdiv(n4, 256), 256, 0, st>>>(reinterpret_cast<const float4*>(si), reinterpret_cast<float4*>(so),
@@ -686,12 +737,20 @@ int gdn_run(const void* q, const void* k, const void* v, const float* g, const v
     static const hipError_t configured = hipFuncSetAttribute(reinterpret_cast<const void*>(gdn_prep),
                                                              hipFuncAttributeMaxDynamicSharedMemorySize, PREP_SMEM);
     if (configured != hipSuccess) return configured;
-    const int NC = (T + C - 1) / C;
-    const Work ws = split(workspace, T, H);
+    int NC = (T + C - 1) / C, nseq = 1;
+    if (gs.n > 0) {
+        nseq = gs.n;
+        gs.chk[0] = 0;
+        for (int i = 0; i < gs.n; i++) gs.chk[i + 1] = gs.chk[i] + (gs.tok[i + 1] - gs.tok[i] + C - 1) / C;
+        NC = gs.chk[gs.n];
+    }
+    if (NC == 0) return hipSuccess;
+    const Work ws = split(workspace, NC, H);
     gdn_prep<<<dim3(NC, H), PT, PREP_SMEM, st>>>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
                                                  static_cast<const bf16*>(v), g, static_cast<const bf16*>(beta), ws, T,
-                                                 H, HK, scale);
-    gdn_scan<<<H * NS, ST, 0, st>>>(ws, ws.decay, static_cast<bf16*>(o), T, H, NC, si, so);
+                                                 H, HK, scale, gs);
+    gdn_scan<<<H * NS * nseq, ST, 0, st>>>(ws, ws.decay, static_cast<bf16*>(o), T, H, NC, si, s_in_stride, so,
+                                          s_out_stride, gs);
     return hipGetLastError();
 }
 
@@ -708,16 +767,33 @@ extern "C" int q35_debug_phase_ticks(unsigned long long* out) {
 
 extern "C" size_t cs1_gdn_workspace_floats(int T, int H) {
     if (T < 0 || H < 0) return 0;
-    return (Layout(T, H).total + 3) / 4;
+    return (Layout((size_t)((T + C - 1) / C), H).total + 3) / 4;
 }
 
 extern "C" int cs1_gdn_prefill(const void* q, const void* k, const void* v, const float* g, const void* beta, void* o,
                                float* workspace, int T, int H, int HK, float scale, void* stream) {
-    return gdn_run(q, k, v, g, beta, o, workspace, T, H, HK, scale, nullptr, nullptr, stream);
+    return gdn_run(q, k, v, g, beta, o, workspace, T, H, HK, scale, nullptr, 0, nullptr, 0, GSeqs{0, {}, {}}, stream);
 }
 
 extern "C" int cs1_gdn_prefill_x(const void* q, const void* k, const void* v, const float* g, const void* beta,
                                  void* o, float* workspace, int T, int H, int HK, float scale, const void* s_in,
                                  void* s_out, void* stream) {
-    return gdn_run(q, k, v, g, beta, o, workspace, T, H, HK, scale, s_in, s_out, stream);
+    return gdn_run(q, k, v, g, beta, o, workspace, T, H, HK, scale, s_in, 0, s_out, 0, GSeqs{0, {}, {}}, stream);
+}
+
+extern "C" int cs1_gdn_prefill_varlen(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                                      void* o, float* workspace, const int32_t* cu_seqlens, int nseq, int H, int HK,
+                                      float scale, const void* s_in, size_t s_in_stride, void* s_out,
+                                      size_t s_out_stride, void* stream) {
+    if (nseq < 0 || nseq > GSEQS_MAX) return hipErrorInvalidValue;
+    if (nseq == 0) return hipSuccess;
+    if (!cu_seqlens || cu_seqlens[0] != 0) return hipErrorInvalidValue;
+    GSeqs gs;
+    gs.n = nseq;
+    for (int i = 0; i <= nseq; i++) {
+        if (i > 0 && cu_seqlens[i] < cu_seqlens[i - 1]) return hipErrorInvalidValue;
+        gs.tok[i] = cu_seqlens[i];
+    }
+    return gdn_run(q, k, v, g, beta, o, workspace, cu_seqlens[nseq], H, HK, scale, s_in, s_in_stride, s_out,
+                   s_out_stride, gs, stream);
 }

@@ -249,6 +249,30 @@ int gemm(Model& m, size_t x, const Tensor& wt, size_t y, int T, int N, int K) {
     return cs1_gemm(m.gemm, sc(m, x), at(m, wt), sc(m, y), T, N, K, N, m.stream);
 }
 
+// Packed Gated DeltaNet over the candidates (groups of up to 64 sequences per launch), every
+// candidate starting from the same captured state.
+int gdn_candidates(Model& m, const Cands* cd, const void* q, const void* k, const void* v, const void* s0,
+                   float scale) {
+    const Q35ModelConfig& c = m.cfg;
+    const size_t n = cd->off.size();
+    for (size_t g0 = 0; g0 < n; g0 += 64) {
+        const size_t g1 = std::min(n, g0 + 64);
+        const int r0 = cd->off[g0];
+        std::vector<int32_t> cu(g1 - g0 + 1);
+        cu[0] = 0;
+        for (size_t i = g0; i < g1; i++) cu[i - g0 + 1] = cu[i - g0] + cd->len[i];
+        const size_t kd = m.w.kd * BF16, vd = m.w.vd * BF16;
+        TRY(cs1_gdn_prefill_varlen(static_cast<const unsigned char*>(q) + r0 * kd,
+                                   static_cast<const unsigned char*>(k) + r0 * kd,
+                                   static_cast<const unsigned char*>(v) + r0 * vd,
+                                   reinterpret_cast<const float*>(sc(m, m.s.g)) + (size_t)r0 * c.lin_v_heads,
+                                   sc(m, m.s.beta) + (size_t)r0 * c.lin_v_heads * BF16, sc(m, m.s.lo) + r0 * vd,
+                                   reinterpret_cast<float*>(sc(m, m.s.ws)), cu.data(), (int)(g1 - g0), c.lin_v_heads,
+                                   c.lin_k_heads, scale, s0, 0, nullptr, 0, m.stream));
+    }
+    return 0;
+}
+
 // The layer stack on T embedded rows (res holds the embeddings). PLAIN: one prompt from
 // position 0. CAPTURE: the same, keeping the per-layer prefix state in m.pre. CANDIDATES:
 // rows are the packed candidates, each continuing the captured prefix at position pre.len.
@@ -276,21 +300,22 @@ int run(Model& m, int T, Mode mode, const Cands* cd) {
                               reinterpret_cast<float*>(sc(m, s.g)), T, hv, st));
             if (mode == CANDIDATES) {
                 // each candidate: three restored prefix rows ahead of its own rows, so the
-                // convolution sees its full history (those three outputs are not used), then
-                // the delta rule from the prefix's final state (model.rs:1421-1470)
-                for (size_t k = 0; k < cd->off.size(); k++) {
+                // convolution sees its full history. The outputs go straight to the packed
+                // rows (cq/ck/cv row 3 + r holds packed row r): a candidate's three history
+                // outputs land in the previous candidate's last rows (or the three pad rows),
+                // so the candidates run last to first and each overwrites them with its own.
+                for (size_t k = cd->off.size(); k-- > 0;) {
                     const int off = cd->off[k], len = cd->len[k];
                     TRY(cs1_copy_dd(sc(m, s.cst), m.pre.mem + m.pre.tail[li], 3 * gw, st));
                     TRY(cs1_copy_dd(sc(m, s.cst) + 3 * gw, base + off * gw, (size_t)len * gw, st));
-                    TRY(cs1_gdn_conv(sc(m, s.cst), ld, at(m, L.conv), sc(m, s.cq), sc(m, s.ck), sc(m, s.cv), len + 3,
-                                     (int)w.kd, (int)w.vd, st));
-                    TRY(cs1_gdn_prefill_x(sc(m, s.cq) + 3 * w.kd * BF16, sc(m, s.ck) + 3 * w.kd * BF16,
-                                          sc(m, s.cv) + 3 * w.vd * BF16,
-                                          reinterpret_cast<const float*>(sc(m, s.g)) + (size_t)off * hv,
-                                          sc(m, s.beta) + (size_t)off * hv * BF16, sc(m, s.lo) + off * w.vd * BF16,
-                                          reinterpret_cast<float*>(sc(m, s.ws)), len, hv, c.lin_k_heads, gdn_scale,
-                                          m.pre.mem + m.pre.state[li], nullptr, st));
+                    TRY(cs1_gdn_conv(sc(m, s.cst), ld, at(m, L.conv), sc(m, s.cq) + (size_t)off * w.kd * BF16,
+                                     sc(m, s.ck) + (size_t)off * w.kd * BF16, sc(m, s.cv) + (size_t)off * w.vd * BF16,
+                                     len + 3, (int)w.kd, (int)w.vd, st));
                 }
+                // the delta rule of all candidates in one packed launch, each from the
+                // prefix's final state (model.rs:1421-1470)
+                TRY(gdn_candidates(m, cd, sc(m, s.cq) + 3 * w.kd * BF16, sc(m, s.ck) + 3 * w.kd * BF16,
+                                   sc(m, s.cv) + 3 * w.vd * BF16, m.pre.mem + m.pre.state[li], gdn_scale));
             } else {
                 TRY(cs1_gdn_conv(base, ld, at(m, L.conv), sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), T, (int)w.kd,
                                  (int)w.vd, st));
@@ -562,7 +587,8 @@ int q35m_create(const Q35ModelConfig* cfg, uint64_t seed, int max_tokens, void**
     s.ln = buf(T * w.vd * BF16);
     s.beta = buf(T * c.lin_v_heads * BF16);
     s.g = buf(T * c.lin_v_heads * 4);
-    s.ws = buf(cs1_gdn_workspace_floats(max_tokens, c.lin_v_heads) * 4);
+    // (packed candidates restart chunks per sequence: up to 64 more chunks per launch)
+    s.ws = buf(cs1_gdn_workspace_floats(max_tokens + 64 * 64, c.lin_v_heads) * 4);
     s.attn_in = buf(T * w.attn_in * BF16);
     s.aq = buf(T * c.heads * c.head_dim * BF16);
     s.agate = buf(T * c.heads * c.head_dim * BF16);

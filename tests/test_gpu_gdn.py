@@ -194,3 +194,55 @@ def test_gdn_zero_inputs_and_tiny_amplitudes_are_finite():
         assert np.isfinite(f).all() and np.isfinite(s).all()
         if amp == 0.0:
             assert not f.any()
+
+
+@pytest.mark.parametrize("shared_state", [True, False])
+def test_gdn_varlen_matches_per_sequence_calls(shared_state):
+    """cs1_gdn_prefill_varlen over packed sequences (empty, partial-chunk and multi-chunk ones)
+    equals one cs1_gdn_prefill_x call per sequence bit for bit, outputs and final states, with
+    one initial state shared by all sequences (the candidate-scoring case) or one each."""
+    api, st = hip.api(), stream()
+    H, HK = 8, 4
+    lens = [0, 1, 63, 64, 65, 200, 129, 0, 7]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    q, k, v, g, beta, _ = cfg0_inputs(T, H, HK, seed=11)
+    rng = np.random.default_rng(12)
+    n = len(lens)
+    states = (rng.standard_normal((1 if shared_state else n, H, D, D)) * 0.05).astype(np.float32)
+    say(f"gdn varlen lens={lens} shared_state={shared_state}")
+    bufs = (dev(q), dev(k), dev(v), dev(g), dev(beta))
+    o = empty(T * H * D * 2)
+    nch = int(sum((x + 63) // 64 for x in lens))
+    ws = empty(api.cs1_gdn_workspace_floats(64 * nch, H) * 4)
+    si = dev(states.reshape(-1))
+    so = empty(n * H * D * D * 4)
+    stride = 0 if shared_state else H * D * D
+    hip.check(api.cs1_gdn_prefill_varlen(*(b.at(0) for b in bufs), o.at(0), ws.at(0), cu.ctypes.data, n, H, HK,
+                                         D ** -0.5, si.at(0), stride, so.at(0), H * D * D, st.handle), "varlen")
+    got_o = get_bf16(o, T * H * D).reshape(T, H, D)
+    got_s = get(so, np.float32, n * H * D * D).reshape(n, H, D, D)
+    for i, L in enumerate(lens):
+        r0 = int(cu[i])
+        s0 = states[0 if shared_state else i]
+        if L == 0:
+            np.testing.assert_array_equal(got_s[i], s0)
+            continue
+        rows = slice(r0, r0 + L)
+        one_o, one_s = run_gdn(q.reshape(T, HK, D)[rows].reshape(-1), k.reshape(T, HK, D)[rows].reshape(-1),
+                               v.reshape(T, H, D)[rows].reshape(-1), g.reshape(T, H)[rows].reshape(-1),
+                               beta.reshape(T, H)[rows].reshape(-1), L, H, HK, s_in=s0, want_state=True)
+        np.testing.assert_array_equal(got_o[rows], one_o)
+        np.testing.assert_array_equal(got_s[i], one_s)
+
+
+def test_gdn_varlen_arguments():
+    api, st = hip.api(), stream()
+    cu = np.array([0, 64, 32], np.int32)  # decreasing
+    assert api.cs1_gdn_prefill_varlen(None, None, None, None, None, None, None, cu.ctypes.data, 2, 8, 4, 1.0, None, 0,
+                                      None, 0, st.handle) != 0
+    cu = np.zeros(66, np.int32)
+    assert api.cs1_gdn_prefill_varlen(None, None, None, None, None, None, None, cu.ctypes.data, 65, 8, 4, 1.0, None, 0,
+                                      None, 0, st.handle) != 0
+    assert api.cs1_gdn_prefill_varlen(None, None, None, None, None, None, None, None, 0, 8, 4, 1.0, None, 0, None, 0,
+                                      st.handle) == 0
