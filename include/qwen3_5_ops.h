@@ -170,6 +170,18 @@ int cs1_attention_varlen(const void* q, const void* k, const void* v, int ldv, c
                          float* lse, const int32_t* cu_seqlens, int nseq, int Hq, int Hk, int Dh, float scale,
                          void* stream);
 
+/* cs1_attention_varlen for packed sequences that all continue one shared prefix (the
+ * candidate scoring of the reference executor, model.rs:1495-1554, which attends each
+ * candidate to the cached prefix K/V): pre (a multiple of 64) prefix rows whose post-prep K
+ * is kp (rows of Hk * Dh) and V is vp (rows of ldvp).  Sequence s is rows [cu_seqlens[s],
+ * cu_seqlens[s + 1]) of q, k, v, gate and out at positions pre, pre + 1, ...: its queries
+ * attend to the prefix keys and, causally, its own; lse is [Hq, cu_seqlens[nseq]].  Each
+ * sequence's result equals cs1_attention_ex on [prefix K/V | its K/V] with q_base = pre bit
+ * for bit.  No K/V copies; one launch per 64 sequences. */
+int cs1_attention_prefix_varlen(const void* q, const void* k, const void* v, int ldv, const void* kp, const void* vp,
+                                int ldvp, int pre, const void* gate, void* out, float* lse, const int32_t* cu_seqlens,
+                                int nseq, int Hq, int Hk, int Dh, float scale, void* stream);
+
 /* Varlen form of cs1_gdn_prefill_x for packed sequences (the candidate-packed prefill of the
  * reference's scoring path, model.rs:1421-1470, which runs the delta rule per candidate):
  * cu_seqlens is a HOST array of nseq + 1 (at most 64) nondecreasing row offsets with

@@ -224,9 +224,16 @@ __device__ unsigned long long q35_fa_ticks[8];
 // s is rows cu[s] .. cu[s + 1] - 1 of q, k, v, gate and out, causal within itself; its
 // blocks are blockIdx.x in [blk[s], blk[s + 1]). n == 0: one sequence of T rows.
 constexpr int SEQS_MAX = 64;
+// With a shared prefix (pre > 0, a multiple of 64): sequence s continues pre prefix rows
+// whose post-prep K and V are kp (rows of Hk * D) and vp (rows of ldvp): its queries are its
+// own rows at positions pre .. pre + len - 1, its keys positions 0 .. pre - 1 from the prefix
+// and pre .. from its own rows.
 struct Seqs {
     int n, lse_ld;
     int cu[SEQS_MAX + 1], blk[SEQS_MAX + 1];
+    int pre, ldvp;
+    const bf16* kp;
+    const bf16* vp;
 };
 
 template <int D, bool GATED, bool GQA4>
@@ -241,15 +248,18 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
         int sq = 0;
         while (sq + 1 < seqs.n && b >= seqs.blk[sq + 1]) sq++;
         b -= seqs.blk[sq];
-        const int r0 = seqs.cu[sq];
-        T = seqs.cu[sq + 1] - r0;
+        // rows are addressed by position: position P + i is the sequence's row i
+        const int r0 = seqs.cu[sq], P = seqs.pre;
+        T = seqs.cu[sq + 1] - r0 + P;
+        q_base = P;
         lse_ld = seqs.lse_ld;
-        q += (size_t)r0 * Hq * D;
-        k += (size_t)r0 * Hk * D;
-        v += (size_t)r0 * ldv;
-        if (GATED) gate += (size_t)r0 * Hq * D;
-        out += (size_t)r0 * Hq * D;
-        if (lse != nullptr) lse += r0;
+        const ptrdiff_t sh = (ptrdiff_t)r0 - P;
+        q += sh * Hq * D;
+        k += sh * Hk * D;
+        v += sh * ldv;
+        if (GATED) gate += sh * Hq * D;
+        out += sh * Hq * D;
+        if (lse != nullptr) lse += sh;
     }
     constexpr int BN = Cfg::BN, QT = (GQA4 || D == 256) ? 1 : 2;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -303,19 +313,26 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
     // it + 2, then computes tile it. The barrier closing step it - 1 guarantees nobody still
     // reads that other stage, and the one closing step it publishes tile it + 1.
     TileRegs<D> regs;
-    if (ntg > 0) load_tile<D>(regs, kh, vh, ldk, ldv, grp_id * BN, T, tg);
+    // keys below the shared prefix length come from the prefix buffers
+    const bf16* kph = seqs.kp + (size_t)hk * D;
+    const bf16* vph = seqs.vp + (size_t)hk * D;
+    auto load = [&](int k0) {
+        if (k0 < seqs.pre) load_tile<D>(regs, kph, vph, ldk, seqs.ldvp, k0, seqs.pre, tg);
+        else load_tile<D>(regs, kh, vh, ldk, ldv, k0, T, tg);
+    };
+    if (ntg > 0) load(grp_id * BN);
     // Unconditional: the compiler's wait analysis must see the Q fragments complete on every
     // path into the loop, or it waits on the in-loop prefetches before each QK^T MFMA.
     wait_vm_all();
     if (ntg > 0) {
         store_tile<D>(regs, gstage, tg);
-        if (ntg > 1) load_tile<D>(regs, kh, vh, ldk, ldv, (2 + grp_id) * BN, T, tg);
+        if (ntg > 1) load((2 + grp_id) * BN);
     }
     __syncthreads();
     for (int it = 0; it < nt0; it++) {
         if (it + 1 < ntg) {
             store_tile<D>(regs, gstage + ((it + 1) & 1) * Cfg::STAGE, tg);
-            if (it + 2 < ntg) load_tile<D>(regs, kh, vh, ldk, ldv, (2 * (it + 2) + grp_id) * BN, T, tg);
+            if (it + 2 < ntg) load((2 * (it + 2) + grp_id) * BN);
         }
         const int tile = 2 * it + grp_id;
         const bool live = it < ntg;  // wave-uniform
@@ -556,7 +573,9 @@ __device__ __forceinline__ u32x2 read_tr(const unsigned char* p) {
 }
 }  // namespace fa32
 
-template <bool GATED>
+// PREFIX: the launch has a shared prefix (a compile-time flag, so launches without one carry
+// no per-tile selection)
+template <bool GATED, bool PREFIX>
 __global__ void __launch_bounds__(512, 1)
     flash32_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int ldv,
                    const bf16* __restrict__ gate, bf16* __restrict__ out, float* __restrict__ lse, int T, int Hq,
@@ -568,15 +587,18 @@ __global__ void __launch_bounds__(512, 1)
         int sq = 0;
         while (sq + 1 < seqs.n && b >= seqs.blk[sq + 1]) sq++;
         b -= seqs.blk[sq];
-        const int r0 = seqs.cu[sq];
-        T = seqs.cu[sq + 1] - r0;
+        // rows are addressed by position: position P + i is the sequence's row i
+        const int r0 = seqs.cu[sq], P = seqs.pre;
+        T = seqs.cu[sq + 1] - r0 + P;
+        q_base = P;
         lse_ld = seqs.lse_ld;
-        q += (size_t)r0 * Hq * D;
-        k += (size_t)r0 * Hk * D;
-        v += (size_t)r0 * ldv;
-        if (GATED) gate += (size_t)r0 * Hq * D;
-        out += (size_t)r0 * Hq * D;
-        if (lse != nullptr) lse += r0;
+        const ptrdiff_t sh = (ptrdiff_t)r0 - P;
+        q += sh * Hq * D;
+        k += sh * Hk * D;
+        v += sh * ldv;
+        if (GATED) gate += sh * Hq * D;
+        out += sh * Hq * D;
+        if (lse != nullptr) lse += sh;
     }
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -613,15 +635,28 @@ __global__ void __launch_bounds__(512, 1)
 #pragma unroll
     for (int j = 0; j < 2; j++) kvoff[j] = drow * ldk * 2 + (k_slot(8 * gw + 4 * j + drow, dslot) << 4);
     vvoff[0] = drow * ldv * 2 + (v_slot(drow, dslot) << 4);
+    int vvoff_p[1] = {drow * seqs.ldvp * 2 + (v_slot(drow, dslot) << 4)};
     // the group's four waves move one tile each of K and V as eight four-row instructions
     // tile j of the group goes to stage sidx = j % 4 (passed separately: a constant in the
     // unrolled main loop)
     const uint32_t gbase = lds_addr(gstage);
+    // keys below the shared prefix length come from the prefix buffers (a tile never
+    // straddles it: the prefix length is a multiple of the tile)
+    const bf16* kph = seqs.kp + (size_t)hk * D;
+    const bf16* vph = seqs.vp + (size_t)hk * D;
     auto dma_k = [&](int j, int sidx, bool valid) {
-        dma(rsrc(kh, ldk, (kg + KG * j) * BN, T, valid), gbase + sidx * STAGE, ldk, gw, kvoff, true);
+        const int k0 = (kg + KG * j) * BN;
+        if (PREFIX && k0 < seqs.pre)
+            dma(rsrc(kph, ldk, k0, seqs.pre, valid), gbase + sidx * STAGE, ldk, gw, kvoff, true);
+        else
+            dma(rsrc(kh, ldk, k0, T, valid), gbase + sidx * STAGE, ldk, gw, kvoff, true);
     };
     auto dma_v = [&](int j, int sidx, bool valid) {
-        dma(rsrc(vh, ldv, (kg + KG * j) * BN, T, valid), gbase + sidx * STAGE + K_BYTES, ldv, gw, vvoff, false);
+        const int k0 = (kg + KG * j) * BN;
+        if (PREFIX && k0 < seqs.pre)
+            dma(rsrc(vph, seqs.ldvp, k0, seqs.pre, valid), gbase + sidx * STAGE + K_BYTES, seqs.ldvp, gw, vvoff_p, false);
+        else
+            dma(rsrc(vh, ldv, k0, T, valid), gbase + sidx * STAGE + K_BYTES, ldv, gw, vvoff, false);
     };
 
     // Pipeline prologue: K(0) and V(-1) (zeros: step 0's P V runs on an empty tile) first, the
@@ -832,17 +867,26 @@ __global__ void __launch_bounds__(512, 1)
     if (lse != nullptr && kg == 0 && hh == 0) lse[(size_t)h * lse_ld + qrow] = (mm + log2f(lt)) * 0.69314718055994531f;
 }
 
-template <bool GATED>
-int launch_flash32(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse, int T,
-                   int Hq, int Hk, float scale, int q_base, int blocks, const Seqs& sq, hipStream_t st) {
-    static const hipError_t configured = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(flash32_kernel<GATED>), hipFuncAttributeMaxDynamicSharedMemorySize, fa32::BYTES);
+template <bool GATED, bool PREFIX>
+int launch_flash32_as(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse,
+                      int T, int Hq, int Hk, float scale, int q_base, int blocks, const Seqs& sq, hipStream_t st) {
+    static const hipError_t configured =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(flash32_kernel<GATED, PREFIX>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, fa32::BYTES);
     if (configured != hipSuccess) return configured;
-    flash32_kernel<GATED><<<blocks, 512, fa32::BYTES, st>>>(
+    flash32_kernel<GATED, PREFIX><<<blocks, 512, fa32::BYTES, st>>>(
         static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
         static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, T, Hq, Hk, scale * 1.4426950408889634f, q_base,
         sq);
     return hipGetLastError();
+}
+
+template <bool GATED>
+int launch_flash32(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse, int T,
+                   int Hq, int Hk, float scale, int q_base, int blocks, const Seqs& sq, hipStream_t st) {
+    return sq.pre > 0 ? launch_flash32_as<GATED, true>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, blocks, sq, st)
+                      : launch_flash32_as<GATED, false>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, blocks, sq,
+                                                        st);
 }
 
 template <int D, bool GATED, bool GQA4>
@@ -857,6 +901,9 @@ int launch_flash(const void* q, const void* k, const void* v, int ldv, const voi
     const int blocks = (T - q_base + nrows - 1) / nrows * (GQA4 ? Hq / 4 : Hq);
     Seqs one;
     one.n = 0;
+    one.pre = 0;
+    one.ldvp = 0;
+    one.kp = one.vp = nullptr;
     if (D == 128 && GQA4)
         return launch_flash32<GATED>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base,
                                      (T - q_base + fa32::ROWS - 1) / fa32::ROWS * (Hq / 4), one, st);
@@ -869,7 +916,8 @@ int launch_flash(const void* q, const void* k, const void* v, int ldv, const voi
 // Packed sequences: groups of up to SEQS_MAX sequences per launch.
 template <int D, bool GATED, bool GQA4>
 int launch_flash_varlen(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse,
-                        const int32_t* cu, int nseq, int Hq, int Hk, float scale, hipStream_t st) {
+                        const int32_t* cu, int nseq, int Hq, int Hk, float scale, int pre, const void* kp,
+                        const void* vp, int ldvp, hipStream_t st) {
     static const hipError_t configured = hipFuncSetAttribute(
         reinterpret_cast<const void*>(flash_kernel<D, GATED, GQA4>), hipFuncAttributeMaxDynamicSharedMemorySize,
         FaCfg<D>::BYTES);
@@ -881,6 +929,10 @@ int launch_flash_varlen(const void* q, const void* k, const void* v, int ldv, co
         Seqs sq;
         sq.n = min(SEQS_MAX, nseq - s0);
         sq.lse_ld = cu[nseq];
+        sq.pre = pre;
+        sq.ldvp = ldvp;
+        sq.kp = static_cast<const bf16*>(kp);
+        sq.vp = static_cast<const bf16*>(vp);
         int blocks = 0;
         for (int i = 0; i < sq.n; i++) {
             sq.cu[i] = cu[s0 + i];
@@ -930,6 +982,39 @@ int attention_run(const void* q, const void* k, const void* v, int ldv, const vo
                 : launch_flash_any<256, false>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, st);
 }
 
+// Packed sequences, optionally continuing a shared prefix (pre rows of kp / vp).
+int attention_varlen_run(const void* q, const void* k, const void* v, int ldv, const void* kp, const void* vp,
+                         int ldvp, int pre, const void* gate, void* out, float* lse, const int32_t* cu_seqlens,
+                         int nseq, int Hq, int Hk, int Dh, float scale, void* stream) {
+    if ((Dh != 128 && Dh != 256) || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || ldv % 8 != 0 || ldv < Hk * Dh || nseq < 0)
+        return hipErrorInvalidValue;
+    if (pre < 0 || pre % 64 != 0) return hipErrorInvalidValue;
+    if (pre > 0 && (!kp || !vp || !aligned16(kp) || !aligned16(vp) || ldvp % 8 != 0 || ldvp < Hk * Dh))
+        return hipErrorInvalidValue;
+    if (nseq == 0) return hipSuccess;
+    if (!cu_seqlens || cu_seqlens[0] != 0) return hipErrorInvalidValue;
+    for (int i = 0; i < nseq; i++)
+        if (cu_seqlens[i + 1] < cu_seqlens[i]) return hipErrorInvalidValue;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || (gate && !aligned16(gate)))
+        return hipErrorInvalidValue;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool g4 = (Hq / Hk) % 4 == 0;
+    auto run = [&](auto d, auto gated) {
+        constexpr int DD = decltype(d)::value;
+        constexpr bool GG = decltype(gated)::value;
+        return g4 ? launch_flash_varlen<DD, GG, true>(q, k, v, ldv, gate, out, lse, cu_seqlens, nseq, Hq, Hk, scale,
+                                                      pre, kp, vp, ldvp, st)
+                  : launch_flash_varlen<DD, GG, false>(q, k, v, ldv, gate, out, lse, cu_seqlens, nseq, Hq, Hk, scale,
+                                                       pre, kp, vp, ldvp, st);
+    };
+    using T128 = std::integral_constant<int, 128>;
+    using T256 = std::integral_constant<int, 256>;
+    using Yes = std::true_type;
+    using No = std::false_type;
+    if (Dh == 128) return gate ? run(T128{}, Yes{}) : run(T128{}, No{});
+    return gate ? run(T256{}, Yes{}) : run(T256{}, No{});
+}
+
 }  // namespace
 }  // namespace q35
 
@@ -944,28 +1029,16 @@ extern "C" int q35_debug_fa_ticks(unsigned long long* out) {
 extern "C" int cs1_attention_varlen(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out,
                                     float* lse, const int32_t* cu_seqlens, int nseq, int Hq, int Hk, int Dh, float scale,
                                     void* stream) {
-    if ((Dh != 128 && Dh != 256) || Hk <= 0 || Hq <= 0 || Hq % Hk != 0 || ldv % 8 != 0 || ldv < Hk * Dh || nseq < 0)
-        return hipErrorInvalidValue;
-    if (nseq == 0) return hipSuccess;
-    if (!cu_seqlens || cu_seqlens[0] != 0) return hipErrorInvalidValue;
-    for (int i = 0; i < nseq; i++)
-        if (cu_seqlens[i + 1] < cu_seqlens[i]) return hipErrorInvalidValue;
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || (gate && !aligned16(gate)))
-        return hipErrorInvalidValue;
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    const bool g4 = (Hq / Hk) % 4 == 0;
-    auto run = [&](auto d, auto gated) {
-        constexpr int DD = decltype(d)::value;
-        constexpr bool GG = decltype(gated)::value;
-        return g4 ? launch_flash_varlen<DD, GG, true>(q, k, v, ldv, gate, out, lse, cu_seqlens, nseq, Hq, Hk, scale, st)
-                  : launch_flash_varlen<DD, GG, false>(q, k, v, ldv, gate, out, lse, cu_seqlens, nseq, Hq, Hk, scale, st);
-    };
-    using T128 = std::integral_constant<int, 128>;
-    using T256 = std::integral_constant<int, 256>;
-    using Yes = std::true_type;
-    using No = std::false_type;
-    if (Dh == 128) return gate ? run(T128{}, Yes{}) : run(T128{}, No{});
-    return gate ? run(T256{}, Yes{}) : run(T256{}, No{});
+    return attention_varlen_run(q, k, v, ldv, nullptr, nullptr, 0, 0, gate, out, lse, cu_seqlens, nseq, Hq, Hk, Dh,
+                                scale, stream);
+}
+
+extern "C" int cs1_attention_prefix_varlen(const void* q, const void* k, const void* v, int ldv, const void* kp,
+                                           const void* vp, int ldvp, int pre, const void* gate, void* out, float* lse,
+                                           const int32_t* cu_seqlens, int nseq, int Hq, int Hk, int Dh, float scale,
+                                           void* stream) {
+    return attention_varlen_run(q, k, v, ldv, kp, vp, ldvp, pre, gate, out, lse, cu_seqlens, nseq, Hq, Hk, Dh, scale,
+                                stream);
 }
 
 extern "C" int cs1_attn_prep(const void* qg, const void* kr, int ld, const void* qw, const void* kw, const void* cos,

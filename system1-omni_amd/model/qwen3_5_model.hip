@@ -147,7 +147,7 @@ struct Widths {
 
 struct Scratch {
     size_t ids, res, x, delta, gdn_in, lq, lk, lv, lo, ln, beta, g, ws, attn_in, aq, agate, ak, ao, gate_up, act,
-        cos, sin, ccos, csin, kwin, vwin, cst, cq, ck, cv, hs, tgt, logits, lp, total;
+        cos, sin, ccos, csin, cst, cq, ck, cv, hs, tgt, logits, lp, total;
 };
 
 // Per-layer state of a captured prompt prefix (offsets into the prefix allocation).
@@ -339,20 +339,20 @@ int run(Model& m, int T, Mode mode, const Cands* cd) {
             TRY(cs1_attn_prep(base, k, ld, at(m, L.q_norm), at(m, L.k_norm), sc(m, co), sc(m, so), sc(m, s.aq),
                               sc(m, s.agate), sc(m, s.ak), T, hq, hk, hd, c.rotary_half, c.eps, st));
             if (mode == CANDIDATES) {
-                // each candidate: keys [prefix K/V | its own], queries its own rows at q_base = P
-                // (the pointers of q, gate and out are based P rows ahead of the candidate;
-                // rows below q_base are never touched) (model.rs:1495-1554)
-                for (size_t j = 0; j < cd->off.size(); j++) {
-                    const int off = cd->off[j], len = cd->len[j];
-                    TRY(cs1_copy_dd(sc(m, s.kwin), m.pre.mem + m.pre.k[ai], (size_t)P * kvb, st));
-                    TRY(cs1_copy_dd(sc(m, s.kwin) + (size_t)P * kvb, sc(m, s.ak) + (size_t)off * kvb, (size_t)len * kvb,
-                                    st));
-                    TRY(cs1_copy_dd(sc(m, s.vwin), m.pre.mem + m.pre.v[ai], (size_t)P * kvb, st));
-                    TRY(cs1_copy2d(sc(m, s.vwin) + (size_t)P * kvb, kvb, v + (size_t)off * aw, aw, kvb, len, st));
-                    const ptrdiff_t q0 = ((ptrdiff_t)off - P) * (ptrdiff_t)qrow;
-                    TRY(cs1_attention_gated_prefix(sc(m, s.aq) + q0, sc(m, s.kwin), sc(m, s.vwin), (int)w.kv,
-                                                   sc(m, s.agate) + q0, sc(m, s.ao) + q0, P + len, hq, hk, hd,
-                                                   att_scale, P, st));
+                // every candidate attends to the cached prefix K/V and, causally, its own rows,
+                // in one packed launch per 64 candidates (model.rs:1495-1554)
+                const size_t n = cd->off.size();
+                for (size_t g0 = 0; g0 < n; g0 += 64) {
+                    const size_t g1 = std::min(n, g0 + 64);
+                    const int r0 = cd->off[g0];
+                    std::vector<int32_t> cu(g1 - g0 + 1);
+                    cu[0] = 0;
+                    for (size_t j = g0; j < g1; j++) cu[j - g0 + 1] = cu[j - g0] + cd->len[j];
+                    TRY(cs1_attention_prefix_varlen(sc(m, s.aq) + r0 * qrow, sc(m, s.ak) + (size_t)r0 * kvb,
+                                                    v + (size_t)r0 * aw, ld, m.pre.mem + m.pre.k[ai],
+                                                    m.pre.mem + m.pre.v[ai], (int)w.kv, P, sc(m, s.agate) + r0 * qrow,
+                                                    sc(m, s.ao) + r0 * qrow, nullptr, cu.data(), (int)(g1 - g0), hq,
+                                                    hk, hd, att_scale, st));
                 }
             } else {
                 if (mode == CAPTURE) {  // post-prep K, raw V (model.rs:1527-1531)
@@ -598,12 +598,10 @@ int q35m_create(const Q35ModelConfig* cfg, uint64_t seed, int max_tokens, void**
     s.act = buf(T * c.intermediate * BF16);
     s.cos = buf(T * c.rotary_half * BF16);
     s.sin = buf(T * c.rotary_half * BF16);
-    // candidate scoring: packed rotary rows, one candidate's K/V window, its conv staging,
+    // candidate scoring: packed rotary rows, one candidate's conv staging and the packed conv outputs,
     // the scored hidden rows, targets, logits and log-probabilities
     s.ccos = buf(T * c.rotary_half * BF16);
     s.csin = buf(T * c.rotary_half * BF16);
-    s.kwin = buf(T * w.kv * BF16);
-    s.vwin = buf(T * w.kv * BF16);
     s.cst = buf((T + 3) * w.gdn_in * BF16);
     s.cq = buf((T + 3) * w.kd * BF16);
     s.ck = buf((T + 3) * w.kd * BF16);

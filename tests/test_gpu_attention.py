@@ -215,3 +215,62 @@ def test_varlen_arguments():
                                     st.handle) == hip.HIP_ERROR_INVALID_VALUE
     assert api.cs1_attention_varlen(None, None, None, 512, None, None, None, None, 0, 16, 4, 128, 0.1,
                                     st.handle) == 0
+
+
+@pytest.mark.parametrize("Dh,hq,hk,gated", [(256, 16, 4, True), (256, 24, 4, True), (128, 16, 4, True),
+                                            (128, 8, 8, False)])
+def test_prefix_varlen_matches_windowed_calls(Dh, hq, hk, gated):
+    """cs1_attention_prefix_varlen (packed candidates continuing one cached prefix) equals, per
+    candidate, cs1_attention_ex over [prefix K/V | candidate K/V] with q_base = prefix length,
+    bit for bit: the candidate-scoring attention without window copies."""
+    api, st = hip.api(), stream()
+    P = 128
+    lens = [1, 40, 64, 100, 0, 33]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    rng = np.random.default_rng(21)
+
+    def bf(n):
+        return O.f32_to_bf16(rng.standard_normal(n).astype(np.float32))
+
+    q, gate = bf(T * hq * Dh), bf(T * hq * Dh)
+    k, v = bf(T * hk * Dh), bf(T * hk * Dh)
+    kp, vp = bf(P * hk * Dh), bf(P * hk * Dh)
+    say(f"attention prefix varlen Dh={Dh} hq={hq} hk={hk} P={P} lens={lens}")
+    out = empty(T * hq * Dh * 2)
+    lse = empty(hq * T * 4)
+    dq, dk, dv, dkp, dvp, dg = (dev(x) for x in (q, k, v, kp, vp, gate))  # held until the results are read
+    hip.check(api.cs1_attention_prefix_varlen(dq.at(0), dk.at(0), dv.at(0), hk * Dh, dkp.at(0), dvp.at(0), hk * Dh, P,
+                                              dg.at(0) if gated else None, out.at(0), lse.at(0), cu.ctypes.data,
+                                              len(lens), hq, hk, Dh, Dh ** -0.5, st.handle), "prefix varlen")
+    got = get_bf16(out, T * hq * Dh).reshape(T, hq, Dh)
+    got_lse = get(lse, np.float32, hq * T).reshape(hq, T)
+    rq, rg = hq * Dh, hk * Dh
+    for i, L in enumerate(lens):
+        if L == 0:
+            continue
+        r0 = int(cu[i])
+        W = P + L
+        kw = np.concatenate([kp, k[r0 * rg:(r0 + L) * rg]])
+        vw = np.concatenate([vp, v[r0 * rg:(r0 + L) * rg]])
+        qw = np.concatenate([np.zeros(P * rq, np.uint16), q[r0 * rq:(r0 + L) * rq]])
+        gw = np.concatenate([np.zeros(P * rq, np.uint16), gate[r0 * rq:(r0 + L) * rq]])
+        one = empty(W * rq * 2)
+        l1 = empty(hq * W * 4)
+        wq, wk, wv, wg = (dev(x) for x in (qw, kw, vw, gw))
+        hip.check(api.cs1_attention_ex(wq.at(0), wk.at(0), wv.at(0), rg, wg.at(0) if gated else None, one.at(0),
+                                       l1.at(0), W, hq, hk, Dh, Dh ** -0.5, P, st.handle), "window")
+        want = get_bf16(one, W * rq).reshape(W, hq, Dh)[P:]
+        np.testing.assert_array_equal(got[r0:r0 + L], want)
+        np.testing.assert_array_equal(got_lse[:, r0:r0 + L], get(l1, np.float32, hq * W).reshape(hq, W)[:, P:])
+
+
+def test_prefix_varlen_arguments():
+    api, st = hip.api(), stream()
+    cu = np.array([0, 8], np.int32)
+    buf = empty(1 << 20)
+    # prefix length not a multiple of 64, missing prefix buffers
+    assert api.cs1_attention_prefix_varlen(buf.at(0), buf.at(0), buf.at(0), 1024, buf.at(0), buf.at(0), 1024, 96, None,
+                                           buf.at(0), None, cu.ctypes.data, 1, 16, 4, 256, 0.1, st.handle) != 0
+    assert api.cs1_attention_prefix_varlen(buf.at(0), buf.at(0), buf.at(0), 1024, None, None, 1024, 64, None,
+                                           buf.at(0), None, cu.ctypes.data, 1, 16, 4, 256, 0.1, st.handle) != 0
