@@ -170,6 +170,17 @@ int cs1_attention_varlen(const void* q, const void* k, const void* v, int ldv, c
                          float* lse, const int32_t* cu_seqlens, int nseq, int Hq, int Hk, int Dh, float scale,
                          void* stream);
 
+/* Varlen form of cs1_gdn_conv for packed sequences that all continue one history (the
+ * per-candidate conv of the reference's scoring path, model.rs:1427-1434 and 1421-1470):
+ * cu_seqlens is a HOST array of nseq + 1 (at most 64) nondecreasing row offsets with
+ * cu_seqlens[0] = 0; sequence s is rows [cu_seqlens[s], cu_seqlens[s + 1]) of qkv (rows of
+ * ld) and of q, k, v.  Each sequence's first outputs see the three rows of hist (rows of ld:
+ * the three pre-conv rows before position 0; null: zeros) as their history, so each result
+ * equals cs1_gdn_conv on [hist | its rows] bit for bit.  Requires 8 | key_dim, value_dim and
+ * ld and 16-byte aligned buffers.  One launch. */
+int cs1_gdn_conv_varlen(const void* qkv, int ld, const void* w, void* q, void* k, void* v, const int32_t* cu_seqlens,
+                        int nseq, const void* hist, int key_dim, int value_dim, void* stream);
+
 /* cs1_attention_varlen for packed sequences that all continue one shared prefix (the
  * candidate scoring of the reference executor, model.rs:1495-1554, which attends each
  * candidate to the cached prefix K/V): pre (a multiple of 64) prefix rows whose post-prep K

@@ -37,15 +37,42 @@ __device__ __forceinline__ void conv_store(bf16* q, bf16* k, bf16* v, int key_di
     *reinterpret_cast<Pack8*>(dst) = y;
 }
 
+// Packed sequences of one conv launch (up to CONV_SEQS_MAX): sequence s is rows tok[s] ..
+// tok[s + 1] - 1 and runs run[s] .. run[s + 1] - 1; every sequence starts from the same three
+// history rows (hist, rows of ld; null: zeros). n == 0: one sequence of T rows, zero history.
+constexpr int CONV_SEQS_MAX = 64;
+struct ConvSeqs {
+    int n;
+    int tok[CONV_SEQS_MAX + 1], run[CONV_SEQS_MAX + 1];
+    const bf16* hist;
+};
+
 // One thread owns 8 consecutive channels for CONV_RUN consecutive tokens. Requires
 // 8 | key_dim, 8 | value_dim, 8 | ld and 16-byte aligned buffers (checked by the host).
 __global__ void __launch_bounds__(THREADS)
     gdn_conv_vec_kernel(const bf16* __restrict__ qkv, int ld, const bf16* __restrict__ w, bf16* __restrict__ q,
-                        bf16* __restrict__ k, bf16* __restrict__ v, int T, int key_dim, int value_dim) {
+                        bf16* __restrict__ k, bf16* __restrict__ v, int T, int key_dim, int value_dim,
+                        const ConvSeqs sq) {
     const int packs = (2 * key_dim + value_dim) / 8;
     const int idx = blockIdx.x * THREADS + threadIdx.x;
-    if (idx >= packs * ((T + CONV_RUN - 1) / CONV_RUN)) return;
-    const int cp = idx % packs, run = idx / packs;
+    const int runs = sq.n > 0 ? sq.run[sq.n] : (T + CONV_RUN - 1) / CONV_RUN;
+    if (idx >= packs * runs) return;
+    const int cp = idx % packs;
+    int run = idx / packs;
+    const bf16* hist = nullptr;
+    if (sq.n > 0) {
+        // packed sequences: this run's sequence (a scan over at most 64) addressed alone
+        int s = 0;
+        while (s + 1 < sq.n && run >= sq.run[s + 1]) s++;
+        run -= sq.run[s];
+        const int r0 = sq.tok[s];
+        T = sq.tok[s + 1] - r0;
+        qkv += (size_t)r0 * ld;
+        q += (size_t)r0 * key_dim;
+        k += (size_t)r0 * key_dim;
+        v += (size_t)r0 * value_dim;
+        hist = sq.hist;
+    }
     const int c = cp * 8, t0 = run * CONV_RUN;
     float wt[8][4];
 #pragma unroll
@@ -66,6 +93,8 @@ __global__ void __launch_bounds__(THREADS)
         const int s = t0 - 3 + r;
         if (s >= 0) {
             unpack8(*reinterpret_cast<const Pack8*>(qkv + (size_t)s * ld + c), win[r]);
+        } else if (hist != nullptr) {
+            unpack8(*reinterpret_cast<const Pack8*>(hist + (size_t)(3 + s) * ld + c), win[r]);
         } else {
 #pragma unroll
             for (int i = 0; i < 8; i++) win[r][i] = 0.f;
@@ -211,14 +240,46 @@ extern "C" int cs1_gdn_conv(const void* qkv, int ld, const void* w, void* q, voi
                      aligned16(q) && aligned16(k) && aligned16(v);
     if (vec) {
         const size_t threads = (size_t)(channels / 8) * ((T + CONV_RUN - 1) / CONV_RUN);
+        ConvSeqs one;
+        one.n = 0;
+        one.hist = nullptr;
         gdn_conv_vec_kernel<<<cdiv(threads, THREADS), THREADS, 0, st>>>(
             static_cast<const bf16*>(qkv), ld, static_cast<const bf16*>(w), static_cast<bf16*>(q),
-            static_cast<bf16*>(k), static_cast<bf16*>(v), T, key_dim, value_dim);
+            static_cast<bf16*>(k), static_cast<bf16*>(v), T, key_dim, value_dim, one);
     } else {
         gdn_conv_scalar_kernel<<<cdiv(n, THREADS), THREADS, 0, st>>>(
             static_cast<const bf16*>(qkv), ld, static_cast<const bf16*>(w), static_cast<bf16*>(q),
             static_cast<bf16*>(k), static_cast<bf16*>(v), T, key_dim, value_dim);
     }
+    return hipGetLastError();
+}
+
+extern "C" int cs1_gdn_conv_varlen(const void* qkv, int ld, const void* w, void* q, void* k, void* v,
+                                   const int32_t* cu_seqlens, int nseq, const void* hist, int key_dim, int value_dim,
+                                   void* stream) {
+    if (nseq < 0 || nseq > CONV_SEQS_MAX || key_dim < 0 || value_dim < 0 || ld < 2 * key_dim + value_dim)
+        return hipErrorInvalidValue;
+    if (nseq == 0) return hipSuccess;
+    if (!cu_seqlens || cu_seqlens[0] != 0) return hipErrorInvalidValue;
+    if (key_dim % 8 != 0 || value_dim % 8 != 0 || ld % 8 != 0 || !aligned16(qkv) || !aligned16(w) || !aligned16(q) ||
+        !aligned16(k) || !aligned16(v) || (hist && !aligned16(hist)))
+        return hipErrorInvalidValue;
+    ConvSeqs sq;
+    sq.n = nseq;
+    sq.hist = static_cast<const bf16*>(hist);
+    sq.tok[0] = 0;
+    sq.run[0] = 0;
+    for (int i = 0; i < nseq; i++) {
+        if (cu_seqlens[i + 1] < cu_seqlens[i]) return hipErrorInvalidValue;
+        sq.tok[i + 1] = cu_seqlens[i + 1];
+        sq.run[i + 1] = sq.run[i] + (cu_seqlens[i + 1] - cu_seqlens[i] + CONV_RUN - 1) / CONV_RUN;
+    }
+    const size_t threads = (size_t)((2 * key_dim + value_dim) / 8) * sq.run[nseq];
+    if (threads == 0) return hipSuccess;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    gdn_conv_vec_kernel<<<cdiv(threads, THREADS), THREADS, 0, st>>>(
+        static_cast<const bf16*>(qkv), ld, static_cast<const bf16*>(w), static_cast<bf16*>(q), static_cast<bf16*>(k),
+        static_cast<bf16*>(v), cu_seqlens[nseq], key_dim, value_dim, sq);
     return hipGetLastError();
 }
 

@@ -147,7 +147,7 @@ struct Widths {
 
 struct Scratch {
     size_t ids, res, x, delta, gdn_in, lq, lk, lv, lo, ln, beta, g, ws, attn_in, aq, agate, ak, ao, gate_up, act,
-        cos, sin, ccos, csin, cst, cq, ck, cv, hs, tgt, logits, lp, total;
+        cos, sin, ccos, csin, hs, tgt, logits, lp, total;
 };
 
 // Per-layer state of a captured prompt prefix (offsets into the prefix allocation).
@@ -249,28 +249,36 @@ int gemm(Model& m, size_t x, const Tensor& wt, size_t y, int T, int N, int K) {
     return cs1_gemm(m.gemm, sc(m, x), at(m, wt), sc(m, y), T, N, K, N, m.stream);
 }
 
-// Packed Gated DeltaNet over the candidates (groups of up to 64 sequences per launch), every
-// candidate starting from the same captured state.
-int gdn_candidates(Model& m, const Cands* cd, const void* q, const void* k, const void* v, const void* s0,
-                   float scale) {
-    const Q35ModelConfig& c = m.cfg;
+// Calls f(first packed row, cu_seqlens) for each group of up to 64 candidates (the packed
+// launches take at most 64 sequences).
+template <class F>
+int for_groups(const Cands* cd, F&& f) {
     const size_t n = cd->off.size();
     for (size_t g0 = 0; g0 < n; g0 += 64) {
         const size_t g1 = std::min(n, g0 + 64);
-        const int r0 = cd->off[g0];
         std::vector<int32_t> cu(g1 - g0 + 1);
         cu[0] = 0;
         for (size_t i = g0; i < g1; i++) cu[i - g0 + 1] = cu[i - g0] + cd->len[i];
-        const size_t kd = m.w.kd * BF16, vd = m.w.vd * BF16;
-        TRY(cs1_gdn_prefill_varlen(static_cast<const unsigned char*>(q) + r0 * kd,
-                                   static_cast<const unsigned char*>(k) + r0 * kd,
-                                   static_cast<const unsigned char*>(v) + r0 * vd,
-                                   reinterpret_cast<const float*>(sc(m, m.s.g)) + (size_t)r0 * c.lin_v_heads,
-                                   sc(m, m.s.beta) + (size_t)r0 * c.lin_v_heads * BF16, sc(m, m.s.lo) + r0 * vd,
-                                   reinterpret_cast<float*>(sc(m, m.s.ws)), cu.data(), (int)(g1 - g0), c.lin_v_heads,
-                                   c.lin_k_heads, scale, s0, 0, nullptr, 0, m.stream));
+        TRY(f(cd->off[g0], cu));
     }
     return 0;
+}
+
+// Packed Gated DeltaNet over the candidates, every candidate starting from the same captured
+// state.
+int gdn_candidates(Model& m, const Cands* cd, const void* q, const void* k, const void* v, const void* s0,
+                   float scale) {
+    const Q35ModelConfig& c = m.cfg;
+    const size_t kd = m.w.kd * BF16, vd = m.w.vd * BF16;
+    return for_groups(cd, [&](int r0, const std::vector<int32_t>& cu) {
+        return cs1_gdn_prefill_varlen(static_cast<const unsigned char*>(q) + r0 * kd,
+                                      static_cast<const unsigned char*>(k) + r0 * kd,
+                                      static_cast<const unsigned char*>(v) + r0 * vd,
+                                      reinterpret_cast<const float*>(sc(m, m.s.g)) + (size_t)r0 * c.lin_v_heads,
+                                      sc(m, m.s.beta) + (size_t)r0 * c.lin_v_heads * BF16, sc(m, m.s.lo) + r0 * vd,
+                                      reinterpret_cast<float*>(sc(m, m.s.ws)), cu.data(), (int)cu.size() - 1,
+                                      c.lin_v_heads, c.lin_k_heads, scale, s0, 0, nullptr, 0, m.stream);
+    });
 }
 
 // The layer stack on T embedded rows (res holds the embeddings). PLAIN: one prompt from
@@ -299,23 +307,18 @@ int run(Model& m, int T, Mode mode, const Cands* cd) {
             TRY(cs1_gdn_gates(b, a, ld, at(m, L.a_log), at(m, L.dt_bias), sc(m, s.beta),
                               reinterpret_cast<float*>(sc(m, s.g)), T, hv, st));
             if (mode == CANDIDATES) {
-                // each candidate: three restored prefix rows ahead of its own rows, so the
-                // convolution sees its full history. The outputs go straight to the packed
-                // rows (cq/ck/cv row 3 + r holds packed row r): a candidate's three history
-                // outputs land in the previous candidate's last rows (or the three pad rows),
-                // so the candidates run last to first and each overwrites them with its own.
-                for (size_t k = cd->off.size(); k-- > 0;) {
-                    const int off = cd->off[k], len = cd->len[k];
-                    TRY(cs1_copy_dd(sc(m, s.cst), m.pre.mem + m.pre.tail[li], 3 * gw, st));
-                    TRY(cs1_copy_dd(sc(m, s.cst) + 3 * gw, base + off * gw, (size_t)len * gw, st));
-                    TRY(cs1_gdn_conv(sc(m, s.cst), ld, at(m, L.conv), sc(m, s.cq) + (size_t)off * w.kd * BF16,
-                                     sc(m, s.ck) + (size_t)off * w.kd * BF16, sc(m, s.cv) + (size_t)off * w.vd * BF16,
-                                     len + 3, (int)w.kd, (int)w.vd, st));
-                }
-                // the delta rule of all candidates in one packed launch, each from the
-                // prefix's final state (model.rs:1421-1470)
-                TRY(gdn_candidates(m, cd, sc(m, s.cq) + 3 * w.kd * BF16, sc(m, s.ck) + 3 * w.kd * BF16,
-                                   sc(m, s.cv) + 3 * w.vd * BF16, m.pre.mem + m.pre.state[li], gdn_scale));
+                // every candidate's convolution sees the prefix's last three pre-conv rows as
+                // its history, then the delta rule runs from the prefix's final state, each in
+                // one packed launch per 64 candidates (model.rs:1421-1470)
+                TRY(for_groups(cd, [&](int r0, const std::vector<int32_t>& cu) {
+                    return cs1_gdn_conv_varlen(base + (size_t)r0 * gw, ld, at(m, L.conv),
+                                               sc(m, s.lq) + (size_t)r0 * w.kd * BF16,
+                                               sc(m, s.lk) + (size_t)r0 * w.kd * BF16,
+                                               sc(m, s.lv) + (size_t)r0 * w.vd * BF16, cu.data(), (int)cu.size() - 1,
+                                               m.pre.mem + m.pre.tail[li], (int)w.kd, (int)w.vd, st);
+                }));
+                TRY(gdn_candidates(m, cd, sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), m.pre.mem + m.pre.state[li],
+                                   gdn_scale));
             } else {
                 TRY(cs1_gdn_conv(base, ld, at(m, L.conv), sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), T, (int)w.kd,
                                  (int)w.vd, st));
@@ -341,19 +344,13 @@ int run(Model& m, int T, Mode mode, const Cands* cd) {
             if (mode == CANDIDATES) {
                 // every candidate attends to the cached prefix K/V and, causally, its own rows,
                 // in one packed launch per 64 candidates (model.rs:1495-1554)
-                const size_t n = cd->off.size();
-                for (size_t g0 = 0; g0 < n; g0 += 64) {
-                    const size_t g1 = std::min(n, g0 + 64);
-                    const int r0 = cd->off[g0];
-                    std::vector<int32_t> cu(g1 - g0 + 1);
-                    cu[0] = 0;
-                    for (size_t j = g0; j < g1; j++) cu[j - g0 + 1] = cu[j - g0] + cd->len[j];
-                    TRY(cs1_attention_prefix_varlen(sc(m, s.aq) + r0 * qrow, sc(m, s.ak) + (size_t)r0 * kvb,
-                                                    v + (size_t)r0 * aw, ld, m.pre.mem + m.pre.k[ai],
-                                                    m.pre.mem + m.pre.v[ai], (int)w.kv, P, sc(m, s.agate) + r0 * qrow,
-                                                    sc(m, s.ao) + r0 * qrow, nullptr, cu.data(), (int)(g1 - g0), hq,
-                                                    hk, hd, att_scale, st));
-                }
+                TRY(for_groups(cd, [&](int r0, const std::vector<int32_t>& cu) {
+                    return cs1_attention_prefix_varlen(sc(m, s.aq) + r0 * qrow, sc(m, s.ak) + (size_t)r0 * kvb,
+                                                       v + (size_t)r0 * aw, ld, m.pre.mem + m.pre.k[ai],
+                                                       m.pre.mem + m.pre.v[ai], (int)w.kv, P,
+                                                       sc(m, s.agate) + r0 * qrow, sc(m, s.ao) + r0 * qrow, nullptr,
+                                                       cu.data(), (int)cu.size() - 1, hq, hk, hd, att_scale, st);
+                }));
             } else {
                 if (mode == CAPTURE) {  // post-prep K, raw V (model.rs:1527-1531)
                     TRY(cs1_copy_dd(m.pre.mem + m.pre.k[ai], sc(m, s.ak), (size_t)T * kvb, st));
@@ -598,14 +595,10 @@ int q35m_create(const Q35ModelConfig* cfg, uint64_t seed, int max_tokens, void**
     s.act = buf(T * c.intermediate * BF16);
     s.cos = buf(T * c.rotary_half * BF16);
     s.sin = buf(T * c.rotary_half * BF16);
-    // candidate scoring: packed rotary rows, one candidate's conv staging and the packed conv outputs,
-    // the scored hidden rows, targets, logits and log-probabilities
+    // candidate scoring: packed rotary rows, the scored hidden rows, targets, logits and
+    // log-probabilities
     s.ccos = buf(T * c.rotary_half * BF16);
     s.csin = buf(T * c.rotary_half * BF16);
-    s.cst = buf((T + 3) * w.gdn_in * BF16);
-    s.cq = buf((T + 3) * w.kd * BF16);
-    s.ck = buf((T + 3) * w.kd * BF16);
-    s.cv = buf((T + 3) * w.vd * BF16);
     s.hs = buf(T * c.hidden * BF16);
     s.tgt = buf(T * 4);
     s.logits = buf(c.lm_head ? T * c.vocab * BF16 : 0);

@@ -77,6 +77,7 @@ SYMBOLS = {
 ADDITIONS = {
     "cs1_attention_ex": (_I, [P, P, P, _I, P, P, P, _I, _I, _I, _I, c_float, _I, P]),
     "cs1_attention_varlen": (_I, [P, P, P, _I, P, P, P, P, _I, _I, _I, _I, c_float, P]),
+    "cs1_gdn_conv_varlen": (_I, [P, _I, P, P, P, P, P, _I, P, _I, _I, P]),
     "cs1_attention_prefix_varlen": (_I, [P, P, P, _I, P, P, _I, _I, P, P, P, P, _I, _I, _I, _I, c_float, P]),
     "cs1_gdn_prefill_varlen": (_I, [P, P, P, P, P, P, P, P, _I, _I, _I, c_float, P, _SZ, P, _SZ, P]),
 }

@@ -216,3 +216,39 @@ def test_embed_and_device_copies():
     src, dst = dev(srcv), empty(rows * w * 2)
     hip.check(api.cs1_copy2d(dst.at(0), w * 2, src.at(0), ld * 2, w * 2, rows, st.handle), "copy2d")
     np.testing.assert_array_equal(get_bf16(dst, rows * w).reshape(rows, w), srcv.reshape(rows, ld)[:, :w])
+
+
+@pytest.mark.parametrize("with_hist", [True, False])
+def test_gdn_conv_varlen_matches_staged_calls(with_hist):
+    """cs1_gdn_conv_varlen over packed sequences (empty, shorter than the window, crossing the
+    16-token runs) equals, per sequence, cs1_gdn_conv on [history rows | its rows] (zero
+    history without hist), bit for bit: the candidate-scoring conv without staging copies."""
+    api, st = hip.api(), stream()
+    key_dim, value_dim = 256, 512
+    ch = 2 * key_dim + value_dim
+    ld = ch + 64
+    lens = [5, 0, 1, 16, 17, 40, 2]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    say(f"gdn_conv_varlen lens={lens} hist={with_hist}")
+    x = rnd(T * ld, 41, 1.0)
+    hist = rnd(3 * ld, 42, 1.0) if with_hist else np.zeros(3 * ld, np.uint16)
+    w = O.f32_to_bf16((np.random.default_rng(3).standard_normal(ch * 4) * 0.5).astype(np.float32))
+    dx, dw, dh = dev(x), dev(w), dev(hist)
+    q, k, v = empty(T * key_dim * 2), empty(T * key_dim * 2), empty(T * value_dim * 2)
+    hip.check(api.cs1_gdn_conv_varlen(dx.at(0), ld, dw.at(0), q.at(0), k.at(0), v.at(0), cu.ctypes.data, len(lens),
+                                      dh.at(0) if with_hist else None, key_dim, value_dim, st.handle), "conv varlen")
+    got = [get_bf16(q, T * key_dim).reshape(T, -1), get_bf16(k, T * key_dim).reshape(T, -1),
+           get_bf16(v, T * value_dim).reshape(T, -1)]
+    for i, L in enumerate(lens):
+        if L == 0:
+            continue
+        r0 = int(cu[i])
+        staged = dev(np.concatenate([hist, x[r0 * ld:(r0 + L) * ld]]))
+        sq, sk, sv = empty((L + 3) * key_dim * 2), empty((L + 3) * key_dim * 2), empty((L + 3) * value_dim * 2)
+        hip.check(api.cs1_gdn_conv(staged.at(0), ld, dw.at(0), sq.at(0), sk.at(0), sv.at(0), L + 3, key_dim, value_dim,
+                                   st.handle), "staged conv")
+        want = [get_bf16(sq, (L + 3) * key_dim).reshape(L + 3, -1)[3:], get_bf16(sk, (L + 3) * key_dim).reshape(L + 3, -1)[3:],
+                get_bf16(sv, (L + 3) * value_dim).reshape(L + 3, -1)[3:]]
+        for g_, w_ in zip(got, want):
+            np.testing.assert_array_equal(g_[r0:r0 + L], w_)
