@@ -470,10 +470,10 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
             if (GATED) {
                 const u32x2 gp =
                     *reinterpret_cast<const u32x2*>(gate + ((size_t)qrow * Hq + h) * D + 16 * dt + 4 * grp);
-                a[0] = round_bf16(a[0]) * round_bf16(sigmoid(lo_f32(gp[0])));
-                a[1] = round_bf16(a[1]) * round_bf16(sigmoid(hi_f32(gp[0])));
-                a[2] = round_bf16(a[2]) * round_bf16(sigmoid(lo_f32(gp[1])));
-                a[3] = round_bf16(a[3]) * round_bf16(sigmoid(hi_f32(gp[1])));
+                a[0] = round_bf16(a[0]) * round_bf16(gate_sigmoid(lo_f32(gp[0])));
+                a[1] = round_bf16(a[1]) * round_bf16(gate_sigmoid(hi_f32(gp[0])));
+                a[2] = round_bf16(a[2]) * round_bf16(gate_sigmoid(lo_f32(gp[1])));
+                a[3] = round_bf16(a[3]) * round_bf16(gate_sigmoid(hi_f32(gp[1])));
             }
             *reinterpret_cast<u32x2*>(dst + 16 * dt) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
         }
@@ -857,10 +857,10 @@ __global__ void __launch_bounds__(512, 1)
             a[r] = acc * inv;
         }
         if (GATED) {
-            a[0] = round_bf16(a[0]) * round_bf16(sigmoid(lo_f32(gp[j][0])));
-            a[1] = round_bf16(a[1]) * round_bf16(sigmoid(hi_f32(gp[j][0])));
-            a[2] = round_bf16(a[2]) * round_bf16(sigmoid(lo_f32(gp[j][1])));
-            a[3] = round_bf16(a[3]) * round_bf16(sigmoid(hi_f32(gp[j][1])));
+            a[0] = round_bf16(a[0]) * round_bf16(gate_sigmoid(lo_f32(gp[j][0])));
+            a[1] = round_bf16(a[1]) * round_bf16(gate_sigmoid(hi_f32(gp[j][0])));
+            a[2] = round_bf16(a[2]) * round_bf16(gate_sigmoid(lo_f32(gp[j][1])));
+            a[3] = round_bf16(a[3]) * round_bf16(gate_sigmoid(hi_f32(gp[j][1])));
         }
         *reinterpret_cast<u32x2*>(out + orow + 8 * j) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
     }

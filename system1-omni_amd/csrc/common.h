@@ -38,6 +38,13 @@ __device__ __forceinline__ float hi_f32(uint32_t p) { return __uint_as_float(p &
 // PyTorch's float32 SiLU and sigmoid: x / (1 + e^-x) and 1 / (1 + e^-x) with expf.
 __device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+// The attention output gate's sigmoid, 1 / (1 + 2^(-x log2 e)), on the hardware exp2 and
+// reciprocal (each within 1 ulp): a few float32 ulps from the expf form, which can move the
+// gate factor by one bf16 step near a rounding boundary. Every gate path (the fused attention
+// epilogues and cs1_sigmoid_gate) uses it, so fused and separate gating agree bit for bit.
+__device__ __forceinline__ float gate_sigmoid(float x) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
 // Butterfly sum over `width` consecutive lanes of a wave64 (width a power of two <= 64).
 template <int width>

@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(THREADS)
 
 // ---- sigmoid gate and SwiGLU ----
 
-__device__ __forceinline__ float gate_factor(bf16 g) { return round_bf16(sigmoid(f32(g))); }
+__device__ __forceinline__ float gate_factor(bf16 g) { return round_bf16(gate_sigmoid(f32(g))); }
 
 __global__ void __launch_bounds__(THREADS) sigmoid_gate_vec_kernel(Pack8* __restrict__ x, const Pack8* __restrict__ gate,
                                                                    size_t n8) {
@@ -176,8 +176,8 @@ __global__ void __launch_bounds__(THREADS) sigmoid_gate_vec_kernel(Pack8* __rest
     const Pack8 gp = gate[i];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        gv[2 * e] = round_bf16(sigmoid(lo_f32(gp.w[e])));
-        gv[2 * e + 1] = round_bf16(sigmoid(hi_f32(gp.w[e])));
+        gv[2 * e] = round_bf16(gate_sigmoid(lo_f32(gp.w[e])));
+        gv[2 * e + 1] = round_bf16(gate_sigmoid(hi_f32(gp.w[e])));
     }
 #pragma unroll
     for (int e = 0; e < 8; e++) xv[e] *= gv[e];

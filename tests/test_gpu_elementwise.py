@@ -191,7 +191,13 @@ def test_sigmoid_gate_vector_and_scalar():
     want = O.sigmoid_gate(x[:n], g[:n])
     dx, dg = dev(x), dev(g)
     hip.check(api.cs1_sigmoid_gate(dx.at(0), dg.at(0), n, st.handle), "vector gate")
-    assert ulp_diff(get_bf16(dx, n), want) <= 1
+    got = get_bf16(dx, n)
+    assert ulp_diff(got, want) <= 1
+    # the gate's sigmoid runs on the hardware exp2 and reciprocal: a gate factor differs from
+    # the expf form only next to a bf16 rounding boundary
+    same = float(np.mean(got == want))
+    say(f"  identical to the expf form: {same:.5f}")
+    assert same >= 0.995
     dx2 = dev(x)
     hip.check(api.cs1_sigmoid_gate(dx2.at(2), dg.at(2), n, st.handle), "scalar gate")
     assert ulp_diff(get_bf16(dx2, n, 2), O.sigmoid_gate(x[1:], g[1:])) <= 1
