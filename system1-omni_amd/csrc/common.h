@@ -45,6 +45,13 @@ __device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + expf(-x)
 __device__ __forceinline__ float gate_sigmoid(float x) {
     return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
+// The GDN conv's SiLU in the same form, x / (1 + 2^(-x log2 e)) with the hardware exp2 and
+// reciprocal; its output is rounded to bf16, so it differs from the expf form by at most one
+// bf16 step, next to a rounding boundary (for x above -87; further down both are -0 or a
+// denormal). It halves the conv's arithmetic, which otherwise bounds that kernel.
+__device__ __forceinline__ float conv_silu(float x) {
+    return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
 // Butterfly sum over `width` consecutive lanes of a wave64 (width a power of two <= 64).
 template <int width>

@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(THREADS)
             acc = fmaf(wt[i][1], win[1][i], acc);
             acc = fmaf(wt[i][2], win[2][i], acc);
             acc = fmaf(wt[i][3], cur[i], acc);
-            y[i] = silu(round_bf16(acc));
+            y[i] = conv_silu(round_bf16(acc));
         }
         conv_store(q, k, v, key_dim, value_dim, t, c, pack8(y));
 #pragma unroll
@@ -139,7 +139,7 @@ __global__ void __launch_bounds__(THREADS)
         const int s = t - 3 + j;
         if (s >= 0) acc = fmaf(f32(w[c * 4 + j]), f32(qkv[(size_t)s * ld + c]), acc);
     }
-    const bf16 y = to_bf16(silu(round_bf16(acc)));
+    const bf16 y = to_bf16(conv_silu(round_bf16(acc)));
     if (c < key_dim)
         q[(size_t)t * key_dim + c] = y;
     else if (c < 2 * key_dim)
