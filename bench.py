@@ -198,13 +198,15 @@ def bench_gdn(api, st, ev, steps, warmup, T, H, HK, with_conv, s0_std, seed, lab
     bufs, launches = gdn_layer(api, st, T, H, HK, with_conv, s0_std, seed)
     wall, per = timed(st, ev, steps, warmup, launches)
     flops = 180224.0 * T * H  # dense-tile count per token per v-head: 10 C D + 6 D^2
+    flops_tri = 139264.0 * T * H  # the same without the upper triangles of A, P and the T products
     io = 2 * T * HK * D * 2 + 2 * T * H * D * 2 + T * H * 6 + (2 if s0_std else 1) * H * D * D * 4
     g_ms = per["gdn_prefill"]
     res = {
         "workload": label, "tokens_per_s": T / (wall * 1e-3), "ms_per_step": wall, "kernel_ms": per,
         "gdn": {"bound": "mfma", "achieved": flops / (g_ms * 1e-3) / 1e12, "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": flops / (g_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-                "algorithmic_flop": flops, "algorithmic_io_bytes": io,
+                "algorithmic_flop": flops, "algorithmic_flop_triangular": flops_tri,
+                "achieved_triangular": flops_tri / (g_ms * 1e-3) / 1e12, "algorithmic_io_bytes": io,
                 "io_GBs": io / (g_ms * 1e-3) / 1e9},
     }
     if with_conv:
@@ -364,6 +366,58 @@ def cpu_baseline_attention():
                       f"emulation of the reference flash kernel, OpenMP over query rows"}
 
 
+def cpu_baseline_gdn_cfg0():
+    """The oracle's C emulation of the reference's chunked GDN prefill (gdn_prefill.cu, with
+    the TF32 pair products and blocked inverse) on this host at config 0, repeated for about
+    5 s (OpenMP over the 16 heads)."""
+    import oracle as O
+
+    T, H, HK = 512, 16, 16
+    rng = np.random.default_rng(0)
+    q, k = unit_rows_bf16(rng, T * HK, 128), unit_rows_bf16(rng, T * HK, 128)
+    v = bf16(rng, T * H * 128)
+    beta = O.f32_to_bf16((1 / (1 + np.exp(-rng.standard_normal(T * H)))).astype(np.float32))
+    g = (-np.log1p(np.exp(rng.standard_normal(T * H))) * 0.1).astype(np.float32)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.gdn_chunk_emul(q, k, v, g, beta, T, H, HK)
+        n += 1
+        if time.perf_counter() - t0 > 5:
+            break
+    dt = time.perf_counter() - t0
+    cores = min(H, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    return {"value": T * n / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"config 0 (T=512, H=HK=16) x{n} through the oracle's C emulation of the reference's "
+                      f"chunked GDN prefill, OpenMP over heads"}
+
+
+def calibrate(st, ev):
+    """The bf16 MFMA and HBM streaming rates this GPU reaches (libq35_calibrate.so, built with
+    the op library), after the same clock settling as every measured region: the published
+    peaks the rooflines use, read against what the machine delivers."""
+    cal = ctypes.CDLL(os.path.join(ROOT, "system1-omni_amd", "libq35_calibrate.so"))
+    cal.q35cal_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    cal.q35cal_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    blocks, iters = 512, 4000  # two waves per SIMD, four independent accumulator chains each
+    out = hip.DeviceBuffer(blocks * 256 * 4)
+    mf = lambda: hip.check(cal.q35cal_mfma(out.at(0), blocks, iters, st.handle), "mfma calibration")  # noqa: E731
+    _, per = timed(st, ev, 5, 1, [("mfma", mf)])
+    flop = 2.0 * 32 * 32 * 16 * 4 * 4 * iters * blocks
+    nbytes = 1 << 30
+    src, dst = hip.DeviceBuffer(nbytes), hip.DeviceBuffer(nbytes)
+    cp = lambda: hip.check(cal.q35cal_copy(src.at(0), dst.at(0), nbytes, st.handle), "copy calibration")  # noqa: E731
+    _, per_c = timed(st, ev, 10, 1, [("copy", cp)])
+    api = hip.api()
+    rt = lambda: hip.check(api.cs1_copy_dd(dst.at(0), src.at(0), nbytes, st.handle), "runtime copy")  # noqa: E731
+    _, per_r = timed(st, ev, 10, 1, [("copy", rt)])
+    return {"mfma_bf16_TFLOPs": flop / (per["mfma"] * 1e-3) / 1e12,
+            "hbm_copy_GBs": 2.0 * nbytes / (per_c["copy"] * 1e-3) / 1e9,
+            "hbm_runtime_copy_GBs": 2.0 * nbytes / (per_r["copy"] * 1e-3) / 1e9,
+            "note": "32x32x16 bf16 MFMA chains (2 waves per SIMD, 4 chains each) and a 1 GiB 16-byte copy "
+                    "(read + write bytes) by this library's kernel and by the runtime's device copy, each after the "
+                    "clock settling"}
+
+
 PROBE_COPY_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_bench_probe.txt")
 
@@ -504,6 +558,9 @@ def main():
     dec_ms, dec = (None, None) if args.no_model else bench_decision_prefill(min(args.steps, 10), args.warmup)
     cand = None if args.no_model else bench_candidates(min(args.steps, 3), 1)
     cpu = None if args.no_cpu else cpu_baseline_attention()
+    if not args.no_cpu:
+        g0["cpu_baseline"] = cpu_baseline_gdn_cfg0()
+    cal = calibrate(st, ev)
     line = {
         "metric": "prefill tokens/s per layer type + ms per 4k-token hybrid decision prefill",
         "value": attn["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -515,6 +572,7 @@ def main():
         "cpu_baseline": cpu,
         "layers": {"attention_cfg1": attn, "attention_t8192": attn8k, "gdn_cfg2": g2, "gdn_cfg0": g0},
         "hbm_ops": hbm,
+        "calibration": cal,
         "decision_prefill_ms_4k": dec_ms,
         "model_cfg3": dec,
         "model_cfg4": cand,
