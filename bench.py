@@ -217,6 +217,68 @@ def bench_gdn(api, st, ev, steps, warmup, T, H, HK, with_conv, s0_std, seed, lab
     return res
 
 
+# The reference's only published timings for this path: its complete cs1_gdn_prefill call on
+# one H200 (benchmarks/gdn/README.md:57-61, the "candidate" wall ms per call, passes 1 / 2).
+H200_GDN_WALL_MS = {107: (0.050914, 0.050957), 936: (0.214176, 0.214178), 3399: (0.696768, 0.697262)}
+
+
+def bench_gdn_reference_shapes(api, st, ev):
+    """The reference harness's GDN benchmark (benchmarks/gdn/artifacts/20261003/kernel/harness/
+    compare.py:76-135) on this GPU: T = 107, 936, 3399 tokens, 16 qk / 48 v heads, seed
+    20261003, k ~ U(-1, 1), q = 0.8 k + 0.2 U, v ~ U, g = (U - 1) 0.01, beta = 0.5 U + 0.5 (numpy's
+    generator, so the same distributions, not the same values). Its protocol: ten warm-up calls,
+    then two passes of 100 complete cs1_gdn_prefill calls each; wall ms per call includes the
+    host submission, the event span is the device time of the 100 calls."""
+    H, HK, D = 48, 16, 128
+    rng = np.random.default_rng(20261003)
+    res = []
+    for T in (107, 936, 3399):
+        u = lambda *shape: rng.random(shape, dtype=np.float32) * 2 - 1  # noqa: E731
+        k = O_bf16(u(T, HK, D))
+        q = O_bf16(0.8 * bf16_f32(k) + 0.2 * bf16_f32(O_bf16(u(T, HK, D))))
+        v = O_bf16(u(T, H, D))
+        g = ((bf16_f32(O_bf16(u(T, H))) - 1) * 0.01).astype(np.float32)
+        beta = O_bf16(bf16_f32(O_bf16(u(T, H))) * 0.5 + 0.5)
+        dq, dk, dv, dg, db = (hip.to_device(np.ascontiguousarray(a).reshape(-1), st) for a in (q, k, v, g, beta))
+        o = hip.DeviceBuffer(T * H * D * 2)
+        ws = hip.DeviceBuffer(api.cs1_gdn_workspace_floats(T, H) * 4)
+
+        def call():
+            hip.check(api.cs1_gdn_prefill(dq.at(0), dk.at(0), dv.at(0), dg.at(0), db.at(0), o.at(0), ws.at(0), T, H,
+                                          HK, D ** -0.5, st.handle), "gdn (reference shapes)")
+
+        settle(st, [("gdn", call)])
+        for _ in range(10):
+            call()
+        st.sync()
+        passes = []
+        for _ in range(2):
+            e0, e1 = ev.new(), ev.new()
+            t0 = time.perf_counter()
+            ev.record(e0, st)
+            for _ in range(100):
+                call()
+            ev.record(e1, st)
+            span = ev.ms(e0, e1) / 100
+            passes.append({"wall_ms_per_call": (time.perf_counter() - t0) * 1e3 / 100, "device_span_ms_per_call": span})
+        wall = sum(p_["wall_ms_per_call"] for p_ in passes) / 2
+        h200 = sum(H200_GDN_WALL_MS[T]) / 2
+        res.append({"tokens": T, "passes": passes, "h200_published_wall_ms": H200_GDN_WALL_MS[T],
+                    "speedup_vs_h200_wall": h200 / wall,
+                    "achieved_TFLOPs_device_span": 180224.0 * T * H / (passes[1]["device_span_ms_per_call"] * 1e-3) / 1e12})
+    return res
+
+
+def O_bf16(x):
+    """float32 -> bf16 bits (round to nearest even)."""
+    u_ = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    return ((u_ + 0x7FFF + ((u_ >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_f32(b):
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
 def bench_hbm_ops(api, st, ev, steps, warmup):
     """The HBM-bound operations around the two layers, each against the HBM peak with its
     algorithmic bytes (read once + written once): the GDN gates and gated RMSNorm at config 2
@@ -555,6 +617,7 @@ def main():
     g0 = bench_gdn(api, st, ev, args.steps, args.warmup, 512, 16, 16, False, 0.0, 0,
                    "cfg0 GDN chunked prefill T=512 H=HK=16 D=128, S0=0")
     hbm = bench_hbm_ops(api, st, ev, args.steps, args.warmup)
+    gref = bench_gdn_reference_shapes(api, st, ev)
     dec_ms, dec = (None, None) if args.no_model else bench_decision_prefill(min(args.steps, 10), args.warmup)
     cand = None if args.no_model else bench_candidates(min(args.steps, 3), 1)
     cpu = None if args.no_cpu else cpu_baseline_attention()
@@ -573,6 +636,7 @@ def main():
         "layers": {"attention_cfg1": attn, "attention_t8192": attn8k, "gdn_cfg2": g2, "gdn_cfg0": g0},
         "hbm_ops": hbm,
         "calibration": cal,
+        "gdn_reference_shapes": gref,
         "decision_prefill_ms_4k": dec_ms,
         "model_cfg3": dec,
         "model_cfg4": cand,
