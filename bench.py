@@ -4,7 +4,7 @@ Metric: "prefill tokens/s per layer type + ms per 4k-token hybri
 decision prefill".  A step is one prefill pass of one layer over one synthetic batch
 with the inputs already resident in HBM:
 
-  * headline (`value`): the gated GQA flash-attention layer of BASELINE config 1
+  * headline (`value`): the gated GQA flash-attention layer of config 1
     (T = 2048, 16 q / 4 kv heads, Dh = 128, sigmoid gate, float32 LSE), tokens/s;
   * `layers`: the same measurement for the GDN layer of config 2 (causal conv1d + SiLU,
     then the chunked gated delta rule, T = 8192, 16 qk / 32 v heads, S0 ~ N(0, 0.01)) and
@@ -323,7 +323,7 @@ def bench_hbm_ops(api, st, ev, steps, warmup):
 
 
 def bench_decision_prefill(steps, warmup, T=4096):
-    """one 4096-token decision prefill of the random-init 4B-class hybrid
+    """Config 3: one 4096-token decision prefill of the random-init 4B-class hybrid
     decoder (32 layers, 3:1 GDN:attention, hidden 2560, SwiGLU 9728, 16/4 x 256 attention,
     GDN 16 qk / 32 v heads) through the native runner, then the 8-label head on the last
     hidden state. A step is one complete q35m_decide call: id upload, embedding, the layer
@@ -367,7 +367,7 @@ def bench_decision_prefill(steps, warmup, T=4096):
 
 
 def bench_candidates(steps, warmup, P=2048, n=8):
-    """the random-init 27B-class hybrid decoder (64 layers, 3:1, hidden
+    """Config 4: the random-init 27B-class hybrid decoder (64 layers, 3:1, hidden
     5120, 24/4 x 256 attention, GDN 16 qk / 48 v heads, SwiGLU 17408, vocabulary 248320, untied
     LM head). A step captures a 2048-token prefix, then scores 8 candidate continuations of
     U[64, 256] tokens (seeded) packed into one pass from the shared prefix state, returning
@@ -628,7 +628,7 @@ def main():
         "metric": "prefill tokens/s per layer type + ms per 4k-token hybrid decision prefill",
         "value": attn["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": attn["ms_per_step"], "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs of the BASELINE shapes)",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs of the benchmark shapes)",
         "config": {"workload": attn["workload"], "global_batch": 1, "seq_len": 2048, "parallelism": "none"},
         "roofline": {k: attn["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac")} |
                     {"traffic": traffic_bytes("q35::(anonymous namespace)::flash32_kernel<true, false> grid=131072 ")},

@@ -56,9 +56,9 @@ class Config:
         return (layer + 1) % self.full_attention_interval == 0
 
 
-# the 4B-class hybrid decoder (32 layers, 3:1 GDN:attention).
+# Config 3: the 4B-class hybrid decoder (32 layers, 3:1 GDN:attention).
 CFG3_4B = Config(layers=32, hidden=2560, intermediate=9728, vocab=151936, heads=16, kv_heads=4)
-# the 27B-class hybrid decoder (64 layers, 3:1), with the remaining sizes
+# Config 4: the 27B-class hybrid decoder (64 layers, 3:1), with the remaining sizes
 # (SwiGLU 17408, vocabulary 248320, untied LM head) from the reference's test config
 # tests/qwen3_5/data/config.json.
 CFG4_27B = Config(layers=64, hidden=5120, intermediate=17408, vocab=248320, heads=24, kv_heads=4, lin_k_heads=16,

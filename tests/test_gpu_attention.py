@@ -1,6 +1,6 @@
 """GPU parity of the causal GQA flash attention (cs1_attention*, cs1_attention_ex).
 
-Mirrors tests/qwen3_5/kernels.rs:273-474 and 852-929 and adds BASELINE config 1
+Mirrors tests/qwen3_5/kernels.rs:273-474 and 852-929 and adds benchmark config 1
 (Dh = 128, sigmoid gate, float32 log-sum-exp), which the reference kernel does not
 support. Bars:
   * vs float64 (kernels.rs:436-472): per (row, head) max|diff| / max(max|ref|, 1e-3) < 1.6e-2;

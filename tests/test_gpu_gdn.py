@@ -1,6 +1,6 @@
 """GPU parity of the chunked Gated DeltaNet prefill (cs1_gdn_prefill{,_x}).
 
-Mirrors tests/qwen3_5/kernels.rs:476-622, 692-742, 931-1088 and adds the BASELINE
+Mirrors tests/qwen3_5/kernels.rs:476-622, 692-742, 931-1088 and adds the benchmark
 configurations. Bars:
   * vs the float64 recurrent reference: max |diff| <= 2e-2 * max |ref| (kernels.rs:620);
   * vs the emulated reference kernel (same rounding points, oracle/oracle.c): bf16 output
@@ -39,7 +39,7 @@ def run_gdn(q, k, v, g, beta, T, H, HK, scale=D ** -0.5, s_in=None, want_state=F
 
 
 def cfg0_inputs(T, H, HK, seed=0, s0_std=0.0):
-    """BASELINE configs 0/2: q, k ~ N(0,1) -> bf16, L2-normalised per head; v ~ N(0,1);
+    """Configs 0 and 2: q, k ~ N(0,1) -> bf16, L2-normalised per head; v ~ N(0,1);
     beta = sigmoid(N(0,1)); g = -softplus(N(0,1)) * 0.1; optional S0 ~ N(0, s0_std)."""
     rng = np.random.default_rng(seed)
 
