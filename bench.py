@@ -494,6 +494,12 @@ def probe(api, st):
     bench_gdn(api, st, ev, 3, 0, 8192, 32, 16, True, 0.01, 2, "cfg2")
     bench_gdn(api, st, ev, 3, 0, 512, 16, 16, False, 0.0, 0, "cfg0")
     bench_hbm_ops(api, st, ev, 3, 0)
+    # the MFMA-bound calibration kernel: the counter pass's reference for a fully busy MFMA
+    cal = ctypes.CDLL(os.path.join(ROOT, "system1-omni_amd", "libq35_calibrate.so"))
+    cal.q35cal_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    out = hip.DeviceBuffer(512 * 256 * 4)
+    for _ in range(3):
+        hip.check(cal.q35cal_mfma(out.at(0), 512, 4000, st.handle), "mfma calibration")
     src, dst = hip.DeviceBuffer(PROBE_COPY_BYTES), hip.DeviceBuffer(PROBE_COPY_BYTES)
     for _ in range(3):
         hip.check(api.cs1_copy_dd(dst.at(0), src.at(0), PROBE_COPY_BYTES, st.handle), "copy")
@@ -514,9 +520,10 @@ def _kernel_base(name):
 
 
 def summarize_pmc(dirs):
-    """Per-kernel averages of FETCH_SIZE / WRITE_SIZE (KiB per dispatch) from rocprofv3
-    counter CSVs of `bench.py --probe`, scaled by the calibration copy: bytes = KiB * scale,
-    scale = copy bytes / the copy's own counter reading."""
+    """Per-kernel averages from rocprofv3 counter CSVs of `bench.py --probe`: FETCH_SIZE /
+    WRITE_SIZE (KiB per dispatch) scaled by the calibration copy (bytes = KiB * scale, scale =
+    copy bytes / the copy's own counter reading), and, where those counters were collected,
+    the MFMA busy fraction and the counted bf16 MFMA flop per dispatch."""
     import csv
     import glob
     from collections import defaultdict
@@ -538,13 +545,29 @@ def summarize_pmc(dirs):
             scale[c] = PROBE_COPY_BYTES / max(got)
             lines.append(f"calibration {c}: copy of {PROBE_COPY_BYTES} B reads {max(got):.0f} KiB -> "
                          f"{scale[c]:.2f} B per counted KiB")
+    # MFMA busy: busy cycles per GPU-active cycle, relative to the calibration kernel (four
+    # independent MFMA chains per wave, which keeps the MFMA units busy)
+    ref = [v["SQ_VALU_MFMA_BUSY_CYCLES"] / v["GRBM_GUI_ACTIVE"] for k, v in avg.items()
+           if "mfma_rate_kernel" in k and v.get("GRBM_GUI_ACTIVE")]
+    if ref:
+        lines.append(f"calibration MFMA: the MFMA-bound kernel reads {ref[0]:.2f} busy cycles per GPU-active "
+                     f"cycle -> mfma_busy 1.000")
     for k, v in sorted(avg.items()):
-        if k.startswith("copy"):
+        if k.startswith("copy") or "mfma_rate_kernel" in k:
             continue
-        f = v.get("FETCH_SIZE", 0.0) * scale.get("FETCH_SIZE", 1024.0)
-        w = v.get("WRITE_SIZE", 0.0) * scale.get("WRITE_SIZE", 1024.0)
-        lines.append(f"traffic {k} fetch_kib={v.get('FETCH_SIZE', float('nan')):.0f} "
-                     f"write_kib={v.get('WRITE_SIZE', float('nan')):.0f} bytes={f + w:.0f}")
+        if "FETCH_SIZE" in v or "WRITE_SIZE" in v:
+            f = v.get("FETCH_SIZE", 0.0) * scale.get("FETCH_SIZE", 1024.0)
+            w = v.get("WRITE_SIZE", 0.0) * scale.get("WRITE_SIZE", 1024.0)
+            lines.append(f"traffic {k} fetch_kib={v.get('FETCH_SIZE', float('nan')):.0f} "
+                         f"write_kib={v.get('WRITE_SIZE', float('nan')):.0f} bytes={f + w:.0f}")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in v and v.get("GRBM_GUI_ACTIVE"):
+            # MFMA busy cycles (summed over the SIMDs) per GPU-active cycle of the serialised
+            # dispatch, as a fraction of the calibration kernel's; MOPS counts bf16 MFMA work in
+            # units of 512 flop
+            busy = v["SQ_VALU_MFMA_BUSY_CYCLES"] / v["GRBM_GUI_ACTIVE"] / ref[0] if ref else float("nan")
+            flop = v.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", float("nan")) * 512
+            lines.append(f"mfma {k} bf16_flop={flop:.4g} busy_cycles={v['SQ_VALU_MFMA_BUSY_CYCLES']:.4g} "
+                         f"gpu_active_cycles={v['GRBM_GUI_ACTIVE']:.4g} mfma_busy={busy:.3f}")
     return "\n".join(lines)
 
 
