@@ -7,20 +7,33 @@
 // matrix; y^T's leading dimension is ldy, so one GEMM can fill a column slice of a wider
 // row-major buffer.
 //
-// Every shape (M, N, K, ldy) gets one plan, built on first use from hipBLASLt's first
-// heuristic choice and then reused, so a given shape always runs the same kernel and its
-// float32 summation order is fixed from call to call. The plans live in the caller-owned
+// Every shape (M, N, K, ldy) gets one plan, built on first use and then reused, so a given
+// shape always runs the same kernel and its float32 summation order is fixed from call to
+// call. On first use outside stream capture the plan is tuned: up to kCandidates of
+// hipBLASLt's heuristic choices are timed on the call's own operands (y is overwritten by
+// each trial and finally by the chosen kernel) and the fastest is kept, unless it beats the
+// first heuristic choice by less than kMargin. Under capture, or with CS1_GEMM_TUNE=0 in the
+// environment, the first heuristic choice is used; CS1_GEMM_TUNE_LOG=1 prints each tuning
+// result to stderr. Tuned choices can differ between processes (they follow measured
+// times), so runs that must be bitwise repeatable across processes set CS1_GEMM_TUNE=0. The plans live in the caller-owned
 // handle, which is not safe for concurrent use (one model drives it from one thread, as
 // the reference's executor does).
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <map>
 #include <tuple>
 
 #include "qwen3_5_ops.h"
 
 namespace {
+
+constexpr int kCandidates = 16;
+constexpr float kMargin = 0.03f;
+constexpr int kTrialWarm = 2, kTrialTimed = 5;
 
 struct Plan {
     hipblasLtMatmulDesc_t op = nullptr;
@@ -48,7 +61,65 @@ void release(Plan& p) {
     p = Plan{};
 }
 
-int build_plan(Gemm& g, int M, int N, int K, int ldy, Plan& p) {
+bool env_flag(const char* name, bool dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    return std::strcmp(v, "0") != 0;
+}
+
+// Average time in ms of one launch of algo on the call's operands, or a negative value if
+// the algorithm fails to run.
+float time_algo(Gemm& g, Plan& p, const hipblasLtMatmulAlgo_t& algo, const void* x, const void* w, void* y,
+                hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+    const float alpha = 1.f, beta = 0.f;
+    for (int i = 0; i < kTrialWarm + kTrialTimed; i++) {
+        if (i == kTrialWarm && hipEventRecord(e0, st) != hipSuccess) return -1.f;
+        if (hipblasLtMatmul(g.handle, p.op, &alpha, w, p.a, x, p.b, &beta, y, p.c, y, p.c, &algo, g.workspace,
+                            g.workspace_bytes, st) != HIPBLAS_STATUS_SUCCESS)
+            return -1.f;
+    }
+    float ms = -1.f;
+    if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+        hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+        return -1.f;
+    return ms / kTrialTimed;
+}
+
+// Picks among the heuristic results r[0..n) by measured time (r[0] unless another is faster
+// by at least kMargin).
+int tune(Gemm& g, Plan& p, const hipblasLtMatmulHeuristicResult_t* r, int n, int M, int N, int K,
+         const void* x, const void* w, void* y, hipStream_t st) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) != hipSuccess) return 0;
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return 0;
+    }
+    // Two rounds over the candidates, each keeping its faster round: the first round also
+    // brings the clock up from idle, which would otherwise penalise the first candidate.
+    float ms[kCandidates];
+    for (int i = 0; i < n; i++) ms[i] = -1.f;
+    for (int round = 0; round < 2; round++)
+        for (int i = 0; i < n; i++) {
+            if (r[i].state != HIPBLAS_STATUS_SUCCESS) continue;
+            const float t = time_algo(g, p, r[i].algo, x, w, y, st, e0, e1);
+            if (t > 0.f && (ms[i] < 0.f || t < ms[i])) ms[i] = t;
+        }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipGetLastError();
+    int best = 0;
+    for (int i = 1; i < n; i++)
+        if (ms[i] > 0.f && (ms[best] <= 0.f || ms[i] < ms[best])) best = i;
+    const int pick = ms[0] > 0.f && ms[best] > ms[0] * (1.f - kMargin) ? 0 : best;
+    if (env_flag("CS1_GEMM_TUNE_LOG", false))
+        std::fprintf(stderr, "cs1_gemm tune M=%d N=%d K=%d: %d candidates, first %.1f us, best %.1f us (#%d), kept #%d\n",
+                     M, N, K, n, ms[0] * 1e3f, ms[best] * 1e3f, best, pick);
+    return pick;
+}
+
+int build_plan(Gemm& g, int M, int N, int K, int ldy, const void* x, const void* w, void* y, hipStream_t st,
+               Plan& p) {
     hipblasStatus_t s = hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F);
     if (s != HIPBLAS_STATUS_SUCCESS) return status(s);
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
@@ -62,21 +133,28 @@ int build_plan(Gemm& g, int M, int N, int K, int ldy, Plan& p) {
     if ((s = hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, K, M, K)) != HIPBLAS_STATUS_SUCCESS) return status(s);
     if ((s = hipblasLtMatrixLayoutCreate(&p.c, HIP_R_16BF, N, M, ldy)) != HIPBLAS_STATUS_SUCCESS) return status(s);
 
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
+    const bool tuning = cap == hipStreamCaptureStatusNone && env_flag("CS1_GEMM_TUNE", true);
+
     hipblasLtMatmulPreference_t pref = nullptr;
     if ((s = hipblasLtMatmulPreferenceCreate(&pref)) != HIPBLAS_STATUS_SUCCESS) return status(s);
     const uint64_t ws = g.workspace_bytes;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
-    hipblasLtMatmulHeuristicResult_t r{};
+    hipblasLtMatmulHeuristicResult_t r[kCandidates]{};
     int found = 0;
-    s = hipblasLtMatmulAlgoGetHeuristic(g.handle, p.op, p.a, p.b, p.c, p.c, pref, 1, &r, &found);
+    s = hipblasLtMatmulAlgoGetHeuristic(g.handle, p.op, p.a, p.b, p.c, p.c, pref, tuning ? kCandidates : 1, r,
+                                        &found);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (s != HIPBLAS_STATUS_SUCCESS) return status(s);
-    if (found == 0 || r.state != HIPBLAS_STATUS_SUCCESS) return status(HIPBLAS_STATUS_NOT_SUPPORTED);
-    p.algo = r.algo;
+    if (found == 0 || r[0].state != HIPBLAS_STATUS_SUCCESS) return status(HIPBLAS_STATUS_NOT_SUPPORTED);
+    const int pick = tuning && found > 1 ? tune(g, p, r, found, M, N, K, x, w, y, st) : 0;
+    p.algo = r[pick].algo;
     return 0;
 }
 
-int plan_for(Gemm& g, int M, int N, int K, int ldy, Plan*& out) {
+int plan_for(Gemm& g, int M, int N, int K, int ldy, const void* x, const void* w, void* y, hipStream_t st,
+             Plan*& out) {
     const Key key{M, N, K, ldy};
     auto it = g.plans.find(key);
     if (it != g.plans.end()) {
@@ -84,7 +162,7 @@ int plan_for(Gemm& g, int M, int N, int K, int ldy, Plan*& out) {
         return 0;
     }
     Plan p;
-    const int rc = build_plan(g, M, N, K, ldy, p);
+    const int rc = build_plan(g, M, N, K, ldy, x, w, y, st, p);
     if (rc != 0) {
         release(p);
         return rc;
@@ -126,7 +204,7 @@ int cs1_gemm(void* gemm, const void* x, const void* w, void* y, int M, int N, in
     if (!g || M < 0 || N <= 0 || K <= 0 || ldy < N) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
     Plan* p = nullptr;
-    const int rc = plan_for(*g, M, N, K, ldy, p);
+    const int rc = plan_for(*g, M, N, K, ldy, x, w, y, static_cast<hipStream_t>(stream), p);
     if (rc != 0) return rc;
     const float alpha = 1.f, beta = 0.f;
     return status(hipblasLtMatmul(g->handle, p->op, &alpha, w, p->a, x, p->b, &beta, y, p->c, y, p->c, &p->algo,
