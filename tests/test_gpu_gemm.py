@@ -106,3 +106,41 @@ def test_gemm_tuned_and_untuned_plans_agree(monkeypatch):
         assert ulp_diff(a[mask], want[mask]) <= 1
         outs.append(a)
     assert ulp_diff(outs[0][mask], outs[1][mask]) <= 1
+
+
+def test_gemm_plan_first_built_under_capture(monkeypatch):
+    """A shape whose first call is recorded into a HIP graph cannot be timed; its plan takes
+    hipBLASLt's first heuristic choice, so every replay equals an eager call of an untuned
+    handle bit for bit (with eager work on the stream between the replays)."""
+    api, st = hip.api(), stream()
+    M, N, K = 96, 384, 640
+    say(f"gemm plan built under capture M={M} N={N} K={K}")
+    rng = np.random.default_rng(23)
+    x = O.f32_to_bf16(rng.standard_normal(M * K).astype(np.float32))
+    w = O.f32_to_bf16((rng.standard_normal(N * K) * 0.05).astype(np.float32))
+    dx, dw, y = dev(x), dev(w), empty(M * N * 2)
+    monkeypatch.setenv("CS1_GEMM_TUNE", "1")
+    h = api.cs1_gemm_create(32 << 20)
+    assert h
+    graph = None
+    try:
+        graph = hip.Graph(st, lambda: hip.check(api.cs1_gemm(h, dx.at(0), dw.at(0), y.at(0), M, N, K, N, st.handle),
+                                                "gemm under capture"))
+        replays = []
+        for i in range(3):
+            hip.upload(y, np.zeros(M * N, np.uint16), st)  # eager work between replays
+            graph.launch(st)
+            replays.append(get_bf16(y, M * N))
+            say(f"  replay {i} done")
+    finally:
+        graph = None
+        api.cs1_gemm_destroy(h)
+    monkeypatch.setenv("CS1_GEMM_TUNE", "0")
+    h0 = api.cs1_gemm_create(32 << 20)
+    assert h0
+    try:
+        want = run(h0, x, w, M, N, K).reshape(-1)
+    finally:
+        api.cs1_gemm_destroy(h0)
+    for r in replays:
+        np.testing.assert_array_equal(r, want)
