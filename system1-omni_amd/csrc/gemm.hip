@@ -148,7 +148,15 @@ int build_plan(Gemm& g, int M, int N, int K, int ldy, const void* x, const void*
     hipblasLtMatmulPreferenceDestroy(pref);
     if (s != HIPBLAS_STATUS_SUCCESS) return status(s);
     if (found == 0 || r[0].state != HIPBLAS_STATUS_SUCCESS) return status(HIPBLAS_STATUS_NOT_SUPPORTED);
-    const int pick = tuning && found > 1 ? tune(g, p, r, found, M, N, K, x, w, y, st) : 0;
+    int pick = 0;
+    if (tuning && found > 1) {
+        // The trials synchronise on events; relaxing this thread's capture mode keeps them from
+        // invalidating a capture that another stream of the thread may have open.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        const bool relaxed = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
+        pick = tune(g, p, r, found, M, N, K, x, w, y, st);
+        if (relaxed) (void)hipThreadExchangeStreamCaptureMode(&mode);
+    }
     p.algo = r[pick].algo;
     return 0;
 }
