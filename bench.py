@@ -361,6 +361,7 @@ def bench_decision_prefill(steps, warmup, T=4096):
             n_gdn * 180224.0 * T * cfg.lin_v_heads)
     return ms, {"workload": "cfg3 random-init 4B-class hybrid decoder (32 layers, 24 GDN + 8 gated attention), "
                             "T=4096 decision prefill + 8-label head, hipGraph replay",
+                "gemm_plans": gemm_plan_mode(),
                 "ms_per_decision": ms, "argmax": int(np.argmax(logits)),
                 "algorithmic_flop": flop, "achieved_TFLOPs": flop / (ms * 1e-3) / 1e12,
                 "frac_of_bf16_peak": flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
@@ -403,8 +404,15 @@ def bench_candidates(steps, warmup, P=2048, n=8):
     return {"workload": "cfg4 random-init 27B-class hybrid decoder (64 layers), 2048-token prefix captured, "
                         f"{n} candidates of {', '.join(str(int(k)) for k in lens)} tokens scored from it",
             "ms_per_job": (cap + sco) * 1e3 / steps, "capture_ms": cap * 1e3 / steps, "score_ms": sco * 1e3 / steps,
-            "candidate_tokens": int(sum(lens)), "best_candidate": int(np.argmax(scores)),
+            "candidate_tokens": int(sum(lens)), "best_candidate": int(np.argmax(scores)), "gemm_plans": gemm_plan_mode(),
             "scores": [round(float(x), 3) for x in scores]}
+
+
+def gemm_plan_mode():
+    """How cs1_gemm picks its hipBLASLt kernels in this process (CS1_GEMM_TUNE)."""
+    if os.environ.get("CS1_GEMM_TUNE") == "0":
+        return "first heuristic choice per shape (CS1_GEMM_TUNE=0)"
+    return "fastest of the top 16 heuristic candidates per shape, timed on first use"
 
 
 def cpu_baseline_attention():
