@@ -69,6 +69,12 @@ void q35m_destroy(void* model);
  * at a length runs eagerly, then captures; later calls at that length replay). */
 int q35m_set_graph(void* model, int enabled);
 
+/* Off by default: every GEMM runs the deterministic plan of cs1_gemm, so results are
+ * bitwise repeatable across processes. When enabled, the first call at each GEMM shape
+ * (outside capture) re-chooses that shape's plan with cs1_gemm_tune: faster on some shapes,
+ * but the kept kernel, and with it the float32 summation order, can differ between processes. */
+int q35m_set_gemm_tuning(void* model, int enabled);
+
 /* Prefill one prompt; writes the final-norm hidden state of the last token (hidden floats).
  * Synchronous: returns after the state is on the host. */
 int q35m_forward(void* model, const int32_t* ids, int T, float* last_hidden);

@@ -129,10 +129,19 @@ int cs1_sigmoid_gate(void* x, const void* gate, size_t n, void* stream);
 int cs1_silu_mul(const void* gate_up, int ld, void* out, int T, int I, void* stream);
 
 /* y [M, N] (rows of ldy) = x [M, K] * w [N, K]^T, bf16 in and out, float32 accumulation,
- * through hipBLASLt with one fixed algorithm per shape.                     ops.h:120-124 */
+ * through hipBLASLt with one fixed algorithm per shape (the first heuristic choice without
+ * atomic split-K accumulation; never waits on the host).                   ops.h:120-124 */
 void* cs1_gemm_create(size_t workspace_bytes);
 void cs1_gemm_destroy(void* gemm);
 int cs1_gemm(void* gemm, const void* x, const void* w, void* y, int M, int N, int K, int ldy, void* stream);
+
+/* Additive (no counterpart in ops.h): cs1_gemm with the shape's plan re-chosen by timing up
+ * to 16 of hipBLASLt's heuristic candidates on these operands, fastest kept (y holds the
+ * kept kernel's result on return). Unlike cs1_gemm it synchronises the stream, so it must
+ * not be called under stream capture (returns hipErrorStreamCaptureUnsupported). The
+ * choice follows measured times, so two processes may keep different kernels for a shape;
+ * without this call every plan is the deterministic first heuristic choice. */
+int cs1_gemm_tune(void* gemm, const void* x, const void* w, void* y, int M, int N, int K, int ldy, void* stream);
 
 /* ---- reference interface: vision tower (ops.h:127-138) ----
  * Out of scope for this build (the vision tower is not on the text prefill path).  The

@@ -7,6 +7,8 @@
 // The layouts are the reference's; the work split is MI355X's: 16-byte accesses per
 // lane, and the conv slides a 4-row window down a run of tokens in registers so every
 // input row is fetched from HBM once.
+#include <algorithm>
+
 #include "common.h"
 
 namespace q35 {
@@ -14,11 +16,16 @@ namespace {
 
 constexpr int THREADS = 256;
 
-__global__ void __launch_bounds__(THREADS) embed_kernel(const int32_t* __restrict__ ids, const Pack8* __restrict__ table,
-                                                        Pack8* __restrict__ out, int packs) {
-    const size_t t = blockIdx.x;
-    const size_t id = (size_t)ids[t];
-    for (int i = threadIdx.x; i < packs; i += blockDim.x) out[t * packs + i] = table[id * packs + i];
+// Embedding gather: the grid is flattened over (token, 16-byte chunk of a row), so
+// consecutive lanes copy consecutive chunks of one row and a row's chunks are spread over
+// as many lanes as it has; each lane copies `per` chunks strided by the grid width.
+__global__ void __launch_bounds__(THREADS) embed_rows(const int32_t* __restrict__ ids, const Pack8* __restrict__ table,
+                                                      Pack8* __restrict__ out, unsigned row_packs, size_t total) {
+    const size_t stride = (size_t)gridDim.x * THREADS;
+    for (size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x; i < total; i += stride) {
+        const size_t row = i / row_packs, col = i - row * row_packs;
+        out[i] = table[(size_t)ids[row] * row_packs + col];
+    }
 }
 
 // ---- causal depthwise conv1d (k = 4) + SiLU ----
@@ -125,42 +132,98 @@ __global__ void __launch_bounds__(THREADS)
     }
 }
 
-// Any shape: one thread per (t, channel).
+// Any shape (unaligned buffers or channel counts not a multiple of 8): one thread per
+// channel and run of CONV_RUN tokens, sliding the same 3-row window as the vector kernel, one
+// bf16 at a time.
 __global__ void __launch_bounds__(THREADS)
-    gdn_conv_scalar_kernel(const bf16* __restrict__ qkv, int ld, const bf16* __restrict__ w, bf16* __restrict__ q,
-                           bf16* __restrict__ k, bf16* __restrict__ v, int T, int key_dim, int value_dim) {
+    gdn_conv_any_kernel(const bf16* __restrict__ qkv, int ld, const bf16* __restrict__ w, bf16* __restrict__ q,
+                        bf16* __restrict__ k, bf16* __restrict__ v, int T, int key_dim, int value_dim) {
     const int channels = 2 * key_dim + value_dim;
+    const int runs = (T + CONV_RUN - 1) / CONV_RUN;
     const size_t idx = (size_t)blockIdx.x * THREADS + threadIdx.x;
-    if (idx >= (size_t)T * channels) return;
-    const int t = (int)(idx / channels), c = (int)(idx % channels);
-    float acc = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int s = t - 3 + j;
-        if (s >= 0) acc = fmaf(f32(w[c * 4 + j]), f32(qkv[(size_t)s * ld + c]), acc);
+    if (idx >= (size_t)runs * channels) return;
+    const int c = (int)(idx % channels), t0 = (int)(idx / channels) * CONV_RUN;
+    bf16* dst;
+    int dld;
+    if (c < key_dim) {
+        dst = q + c;
+        dld = key_dim;
+    } else if (c < 2 * key_dim) {
+        dst = k + (c - key_dim);
+        dld = key_dim;
+    } else {
+        dst = v + (c - 2 * key_dim);
+        dld = value_dim;
     }
-    const bf16 y = to_bf16(conv_silu(round_bf16(acc)));
-    if (c < key_dim)
-        q[(size_t)t * key_dim + c] = y;
-    else if (c < 2 * key_dim)
-        k[(size_t)t * key_dim + c - key_dim] = y;
-    else
-        v[(size_t)t * value_dim + c - 2 * key_dim] = y;
+    const float w0 = f32(w[c * 4]), w1 = f32(w[c * 4 + 1]), w2 = f32(w[c * 4 + 2]), w3 = f32(w[c * 4 + 3]);
+    float h0 = t0 >= 3 ? f32(qkv[(size_t)(t0 - 3) * ld + c]) : 0.f;
+    float h1 = t0 >= 2 ? f32(qkv[(size_t)(t0 - 2) * ld + c]) : 0.f;
+    float h2 = t0 >= 1 ? f32(qkv[(size_t)(t0 - 1) * ld + c]) : 0.f;
+    const int t_end = min(T, t0 + CONV_RUN);
+    for (int t = t0; t < t_end; t++) {
+        const float x = f32(qkv[(size_t)t * ld + c]);
+        // taps in order; a zero (padding) row leaves the sum unchanged
+        const float acc = fmaf(w3, x, fmaf(w2, h2, fmaf(w1, h1, fmaf(w0, h0, 0.f))));
+        dst[(size_t)t * dld] = to_bf16(conv_silu(round_bf16(acc)));
+        h0 = h1;
+        h1 = h2;
+        h2 = x;
+    }
 }
 
 // ---- gates ----
 
+// beta = bf16(sigmoid(b)); g = -exp(A_log) * softplus(a + dt_bias), softplus(x) = x above 20
+// (reference elementwise.cu:50-54; float32, expf/log1pf as PyTorch evaluates them).
+__device__ __forceinline__ void gate_values(float b, float a, float neg_a_exp, float dt, bf16& beta, float& g) {
+    beta = to_bf16(sigmoid(b));
+    const float x = a + dt;
+    g = neg_a_exp * (x > 20.f ? x : log1pf(expf(x)));
+}
+
+// Rows of H heads with H % 8 == 0 and 16-byte aligned operands: a thread takes 8 heads of
+// one token (one 16-byte load of b and of a, one 16-byte beta store, two of g). The head
+// constants are loaded once per thread; threads of a block walk tokens with a grid stride.
 __global__ void __launch_bounds__(THREADS)
-    gdn_gates_kernel(const bf16* __restrict__ b, const bf16* __restrict__ a, int ld, const bf16* __restrict__ A_log,
-                     const bf16* __restrict__ dt_bias, bf16* __restrict__ beta, float* __restrict__ g, int n, int H) {
-    const int i = blockIdx.x * THREADS + threadIdx.x;
-    if (i >= n) return;
-    const int h = i % H;
-    const size_t src = (size_t)(i / H) * ld + h;
-    beta[i] = to_bf16(sigmoid(f32(b[src])));
-    const float x = f32(a[src]) + f32(dt_bias[h]);
-    const float sp = x > 20.f ? x : log1pf(expf(x));
-    g[i] = -expf(f32(A_log[h])) * sp;
+    gdn_gates_vec_kernel(const bf16* __restrict__ b, const bf16* __restrict__ a, int ld,
+                         const bf16* __restrict__ A_log, const bf16* __restrict__ dt_bias, bf16* __restrict__ beta,
+                         float* __restrict__ g, int T, int H) {
+    const int groups = H / 8;
+    const size_t total = (size_t)T * groups;
+    const size_t stride = (size_t)gridDim.x * THREADS;
+    for (size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x; i < total; i += stride) {
+        const size_t t = i / groups;
+        const int h0 = (int)(i - t * groups) * 8;
+        float bv[8], av[8], al[8], dt[8], gv[8];
+        unpack8(*reinterpret_cast<const Pack8*>(b + t * ld + h0), bv);
+        unpack8(*reinterpret_cast<const Pack8*>(a + t * ld + h0), av);
+        unpack8(*reinterpret_cast<const Pack8*>(A_log + h0), al);
+        unpack8(*reinterpret_cast<const Pack8*>(dt_bias + h0), dt);
+        Pack8 out;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            bf16 lo, hi;
+            gate_values(bv[e], av[e], -expf(al[e]), dt[e], lo, gv[e]);
+            gate_values(bv[e + 1], av[e + 1], -expf(al[e + 1]), dt[e + 1], hi, gv[e + 1]);
+            out.w[e / 2] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        *reinterpret_cast<Pack8*>(beta + t * H + h0) = out;
+        f32x4* gp = reinterpret_cast<f32x4*>(g + t * H + h0);
+        gp[0] = f32x4{gv[0], gv[1], gv[2], gv[3]};
+        gp[1] = f32x4{gv[4], gv[5], gv[6], gv[7]};
+    }
+}
+
+// Any H or alignment: one thread per (token, head).
+__global__ void __launch_bounds__(THREADS)
+    gdn_gates_any_kernel(const bf16* __restrict__ b, const bf16* __restrict__ a, int ld,
+                         const bf16* __restrict__ A_log, const bf16* __restrict__ dt_bias, bf16* __restrict__ beta,
+                         float* __restrict__ g, int T, int H) {
+    const size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x;
+    if (i >= (size_t)T * H) return;
+    const size_t t = i / H;
+    const int h = (int)(i - t * H);
+    gate_values(f32(b[t * ld + h]), f32(a[t * ld + h]), -expf(f32(A_log[h])), f32(dt_bias[h]), beta[i], g[i]);
 }
 
 // ---- sigmoid gate and SwiGLU ----
@@ -222,10 +285,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 using namespace q35;
 
 extern "C" int cs1_embed(const int32_t* ids, const void* table, void* out, int T, int D, void* stream) {
-    if (D % 8 != 0 || D < 0) return hipErrorInvalidValue;
-    if (T <= 0 || D == 0) return hipSuccess;
-    embed_kernel<<<T, THREADS, 0, static_cast<hipStream_t>(stream)>>>(ids, static_cast<const Pack8*>(table),
-                                                                      static_cast<Pack8*>(out), D / 8);
+    if (D % 8 != 0 || D < 0 || T < 0) return hipErrorInvalidValue;
+    if (T == 0 || D == 0) return hipSuccess;
+    if (!aligned16(table) || !aligned16(out)) return hipErrorInvalidValue;
+    const size_t total = (size_t)T * (D / 8);
+    const unsigned blocks = (unsigned)std::min<size_t>(cdiv(total, THREADS), 2048);
+    embed_rows<<<blocks, THREADS, 0, static_cast<hipStream_t>(stream)>>>(ids, static_cast<const Pack8*>(table),
+                                                                        static_cast<Pack8*>(out), D / 8, total);
     return hipGetLastError();
 }
 
@@ -247,7 +313,8 @@ extern "C" int cs1_gdn_conv(const void* qkv, int ld, const void* w, void* q, voi
             static_cast<const bf16*>(qkv), ld, static_cast<const bf16*>(w), static_cast<bf16*>(q),
             static_cast<bf16*>(k), static_cast<bf16*>(v), T, key_dim, value_dim, one);
     } else {
-        gdn_conv_scalar_kernel<<<cdiv(n, THREADS), THREADS, 0, st>>>(
+        const size_t threads = (size_t)channels * ((T + CONV_RUN - 1) / CONV_RUN);
+        gdn_conv_any_kernel<<<cdiv(threads, THREADS), THREADS, 0, st>>>(
             static_cast<const bf16*>(qkv), ld, static_cast<const bf16*>(w), static_cast<bf16*>(q),
             static_cast<bf16*>(k), static_cast<bf16*>(v), T, key_dim, value_dim);
     }
@@ -286,11 +353,19 @@ extern "C" int cs1_gdn_conv_varlen(const void* qkv, int ld, const void* w, void*
 extern "C" int cs1_gdn_gates(const void* b, const void* a, int ld, const void* A_log, const void* dt_bias, void* beta,
                              float* g, int T, int H, void* stream) {
     if (T < 0 || H < 0 || ld < H) return hipErrorInvalidValue;
-    const int n = T * H;
+    const size_t n = (size_t)T * H;
     if (n == 0) return hipSuccess;
-    gdn_gates_kernel<<<cdiv(n, THREADS), THREADS, 0, static_cast<hipStream_t>(stream)>>>(
-        static_cast<const bf16*>(b), static_cast<const bf16*>(a), ld, static_cast<const bf16*>(A_log),
-        static_cast<const bf16*>(dt_bias), static_cast<bf16*>(beta), g, n, H);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const bf16 *pb = static_cast<const bf16*>(b), *pa = static_cast<const bf16*>(a);
+    const bf16 *pl = static_cast<const bf16*>(A_log), *pd = static_cast<const bf16*>(dt_bias);
+    if (H % 8 == 0 && ld % 8 == 0 && aligned16(b) && aligned16(a) && aligned16(A_log) && aligned16(dt_bias) &&
+        aligned16(beta) && aligned16(g)) {
+        const unsigned blocks = (unsigned)std::min<size_t>(cdiv(n / 8, THREADS), 1024);
+        gdn_gates_vec_kernel<<<blocks, THREADS, 0, st>>>(pb, pa, ld, pl, pd, static_cast<bf16*>(beta), g, T, H);
+    } else {
+        gdn_gates_any_kernel<<<cdiv(n, THREADS), THREADS, 0, st>>>(pb, pa, ld, pl, pd, static_cast<bf16*>(beta), g, T,
+                                                                   H);
+    }
     return hipGetLastError();
 }
 

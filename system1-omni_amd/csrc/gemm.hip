@@ -9,23 +9,32 @@
 //
 // Every shape (M, N, K, ldy) gets one plan, built on first use and then reused, so a given
 // shape always runs the same kernel and its float32 summation order is fixed from call to
-// call. On first use outside stream capture the plan is tuned: up to kCandidates of
-// hipBLASLt's heuristic choices are timed on the call's own operands (y is overwritten by
-// each trial and finally by the chosen kernel) and the fastest is kept, unless it beats the
-// first heuristic choice by less than kMargin. Under capture, or with CS1_GEMM_TUNE=0 in the
-// environment, the first heuristic choice is used; CS1_GEMM_TUNE_LOG=1 prints each tuning
-// result to stderr. Tuned choices can differ between processes (they follow measured
-// times), so runs that must be bitwise repeatable across processes set CS1_GEMM_TUNE=0. The plans live in the caller-owned
-// handle, which is not safe for concurrent use (one model drives it from one thread, as
-// the reference's executor does).
+// call. cs1_gemm itself never waits on the host: a new plan is hipBLASLt's first heuristic
+// choice that it accepts at launch (a stream-K kernel can be listed and then refused for the
+// handle's workspace) among the kernels that do not accumulate split-K partial sums into the
+// output with atomics (the reference excludes in-place split-K reductions for the same reason,
+// gemm.cu:63-80), so the plan, and with it every result bit, is the same in every process
+// on the same device and library.
+//
+// cs1_gemm_tune is the additive, explicit alternative for callers that prefer speed over
+// cross-process repeatability: it times up to kCandidates heuristic choices on the call's
+// own operands (y is overwritten by each trial and finally by the kept kernel), keeps the
+// fastest unless it beats the default by less than kMargin, and synchronises the stream to
+// do so, so it must run before any capture. A tuned choice follows measured times and can
+// differ between processes. The plans live in the caller-owned handle, which is not safe
+// for concurrent use (one model drives it from one thread, as the reference's executor
+// does). CS1_GEMM_LOG=1 prints each plan's kernel to stderr.
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <string>
 #include <tuple>
+#include <vector>
 
 #include "qwen3_5_ops.h"
 
@@ -39,6 +48,12 @@ struct Plan {
     hipblasLtMatmulDesc_t op = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
     hipblasLtMatmulAlgo_t algo{};
+    // Until a launch succeeds, the later heuristic choices (in heuristic order) that replace
+    // algo if hipBLASLt rejects it at launch; a host-side rejection depends only on the shape,
+    // the workspace size and the library, so the kernel a shape settles on is the same in
+    // every process.
+    std::vector<hipblasLtMatmulAlgo_t> fallback;
+    bool settled = false;
 };
 
 using Key = std::tuple<int, int, int, int>;  // M, N, K, ldy
@@ -118,8 +133,7 @@ int tune(Gemm& g, Plan& p, const hipblasLtMatmulHeuristicResult_t* r, int n, int
     return pick;
 }
 
-int build_plan(Gemm& g, int M, int N, int K, int ldy, const void* x, const void* w, void* y, hipStream_t st,
-               Plan& p) {
+int describe(int M, int N, int K, int ldy, Plan& p) {
     hipblasStatus_t s = hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F);
     if (s != HIPBLAS_STATUS_SUCCESS) return status(s);
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
@@ -132,52 +146,74 @@ int build_plan(Gemm& g, int M, int N, int K, int ldy, const void* x, const void*
     if ((s = hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, K, N, K)) != HIPBLAS_STATUS_SUCCESS) return status(s);
     if ((s = hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, K, M, K)) != HIPBLAS_STATUS_SUCCESS) return status(s);
     if ((s = hipblasLtMatrixLayoutCreate(&p.c, HIP_R_16BF, N, M, ldy)) != HIPBLAS_STATUS_SUCCESS) return status(s);
-
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
-    const bool tuning = cap == hipStreamCaptureStatusNone && env_flag("CS1_GEMM_TUNE", true);
-
-    hipblasLtMatmulPreference_t pref = nullptr;
-    if ((s = hipblasLtMatmulPreferenceCreate(&pref)) != HIPBLAS_STATUS_SUCCESS) return status(s);
-    const uint64_t ws = g.workspace_bytes;
-    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
-    hipblasLtMatmulHeuristicResult_t r[kCandidates]{};
-    int found = 0;
-    s = hipblasLtMatmulAlgoGetHeuristic(g.handle, p.op, p.a, p.b, p.c, p.c, pref, tuning ? kCandidates : 1, r,
-                                        &found);
-    hipblasLtMatmulPreferenceDestroy(pref);
-    if (s != HIPBLAS_STATUS_SUCCESS) return status(s);
-    if (found == 0 || r[0].state != HIPBLAS_STATUS_SUCCESS) return status(HIPBLAS_STATUS_NOT_SUPPORTED);
-    int pick = 0;
-    if (tuning && found > 1) {
-        // The trials synchronise on events; relaxing this thread's capture mode keeps them from
-        // invalidating a capture that another stream of the thread may have open.
-        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
-        const bool relaxed = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
-        pick = tune(g, p, r, found, M, N, K, x, w, y, st);
-        if (relaxed) (void)hipThreadExchangeStreamCaptureMode(&mode);
-    }
-    p.algo = r[pick].algo;
     return 0;
 }
 
-int plan_for(Gemm& g, int M, int N, int K, int ldy, const void* x, const void* w, void* y, hipStream_t st,
-             Plan*& out) {
-    const Key key{M, N, K, ldy};
-    auto it = g.plans.find(key);
-    if (it != g.plans.end()) {
-        out = &it->second;
-        return 0;
+// Kernels whose split-K partial sums meet in the output through atomic adds: their
+// summation order, and so the rounding, changes from run to run. hipBLASLt names the
+// global-split-U algorithm of a kernel in its name ("GSUASB": single buffer, atomic
+// accumulation); the multiple-buffer form reduces through the workspace in a fixed order.
+bool accumulates_atomically(Gemm& g, hipblasLtMatmulAlgo_t& algo) {
+    const std::string name = hipblaslt_ext::getKernelNameFromAlgo(g.handle, algo);
+    return name.find("GSUASB") != std::string::npos;
+}
+
+// Up to want heuristic results for the plan's shape, atomically accumulating kernels removed;
+// returns their count in *n.
+int candidates(Gemm& g, Plan& p, int want, hipblasLtMatmulHeuristicResult_t* r, int* n) {
+    hipblasLtMatmulPreference_t pref = nullptr;
+    hipblasStatus_t s = hipblasLtMatmulPreferenceCreate(&pref);
+    if (s != HIPBLAS_STATUS_SUCCESS) return status(s);
+    const uint64_t ws = g.workspace_bytes;
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
+    hipblasLtMatmulHeuristicResult_t all[kCandidates]{};
+    int found = 0;
+    s = hipblasLtMatmulAlgoGetHeuristic(g.handle, p.op, p.a, p.b, p.c, p.c, pref, kCandidates, all, &found);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    if (s != HIPBLAS_STATUS_SUCCESS) return status(s);
+    int k = 0;
+    for (int i = 0; i < found && k < want; i++) {
+        if (all[i].state == HIPBLAS_STATUS_SUCCESS && all[i].workspaceSize <= g.workspace_bytes &&
+            !accumulates_atomically(g, all[i].algo))
+            r[k++] = all[i];
     }
+    *n = k;
+    return k == 0 ? status(HIPBLAS_STATUS_NOT_SUPPORTED) : 0;
+}
+
+void log_plan(Gemm& g, Plan& p, int M, int N, int K, const char* how) {
+    if (!env_flag("CS1_GEMM_LOG", false)) return;
+    std::fprintf(stderr, "cs1_gemm plan M=%d N=%d K=%d (%s): %s\n", M, N, K, how,
+                 hipblaslt_ext::getKernelNameFromAlgo(g.handle, p.algo).c_str());
+}
+
+int new_plan(Gemm& g, int M, int N, int K, int ldy, Plan*& out) {
     Plan p;
-    const int rc = build_plan(g, M, N, K, ldy, x, w, y, st, p);
+    int rc = describe(M, N, K, ldy, p);
+    hipblasLtMatmulHeuristicResult_t r[kCandidates]{};
+    int n = 0;
+    if (rc == 0) rc = candidates(g, p, kCandidates, r, &n);
     if (rc != 0) {
         release(p);
         return rc;
     }
-    out = &g.plans.emplace(key, p).first->second;
+    p.algo = r[0].algo;
+    for (int i = 1; i < n; i++) p.fallback.push_back(r[i].algo);
+    log_plan(g, p, M, N, K, "first choice");
+    out = &g.plans.emplace(Key{M, N, K, ldy}, p).first->second;
     return 0;
 }
+
+int plan_for(Gemm& g, int M, int N, int K, int ldy, Plan*& out) {
+    auto it = g.plans.find(Key{M, N, K, ldy});
+    if (it != g.plans.end()) {
+        out = &it->second;
+        return 0;
+    }
+    return new_plan(g, M, N, K, ldy, out);
+}
+
+bool valid(const Gemm* g, int M, int N, int K, int ldy) { return g && M >= 0 && N > 0 && K > 0 && ldy >= N; }
 
 }  // namespace
 
@@ -209,14 +245,50 @@ void cs1_gemm_destroy(void* gemm) {
 
 int cs1_gemm(void* gemm, const void* x, const void* w, void* y, int M, int N, int K, int ldy, void* stream) {
     Gemm* g = static_cast<Gemm*>(gemm);
-    if (!g || M < 0 || N <= 0 || K <= 0 || ldy < N) return hipErrorInvalidValue;
+    if (!valid(g, M, N, K, ldy)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
     Plan* p = nullptr;
-    const int rc = plan_for(*g, M, N, K, ldy, x, w, y, static_cast<hipStream_t>(stream), p);
+    const int rc = plan_for(*g, M, N, K, ldy, p);
     if (rc != 0) return rc;
     const float alpha = 1.f, beta = 0.f;
-    return status(hipblasLtMatmul(g->handle, p->op, &alpha, w, p->a, x, p->b, &beta, y, p->c, y, p->c, &p->algo,
-                                  g->workspace, g->workspace_bytes, static_cast<hipStream_t>(stream)));
+    for (;;) {
+        const hipblasStatus_t s = hipblasLtMatmul(g->handle, p->op, &alpha, w, p->a, x, p->b, &beta, y, p->c, y,
+                                                  p->c, &p->algo, g->workspace, g->workspace_bytes,
+                                                  static_cast<hipStream_t>(stream));
+        if (s == HIPBLAS_STATUS_SUCCESS) {
+            p->settled = true;
+            return 0;
+        }
+        if (p->settled || p->fallback.empty()) return status(s);
+        p->algo = p->fallback.front();
+        p->fallback.erase(p->fallback.begin());
+        log_plan(*g, *p, M, N, K, "next choice after a rejected launch");
+    }
+}
+
+int cs1_gemm_tune(void* gemm, const void* x, const void* w, void* y, int M, int N, int K, int ldy, void* stream) {
+    Gemm* g = static_cast<Gemm*>(gemm);
+    if (!valid(g, M, N, K, ldy)) return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(st, &cap);
+    if (e != hipSuccess) return e;
+    if (cap != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+    Plan* p = nullptr;
+    int rc = plan_for(*g, M, N, K, ldy, p);
+    if (rc != 0) return rc;
+    hipblasLtMatmulHeuristicResult_t r[kCandidates]{};
+    int n = 0;
+    if ((rc = candidates(*g, *p, kCandidates, r, &n)) != 0) return rc;
+    const int pick = n > 1 ? tune(*g, *p, r, n, M, N, K, x, w, y, st) : 0;
+    p->algo = r[pick].algo;
+    p->fallback.clear();
+    for (int i = 0; i < n; i++)
+        if (i != pick) p->fallback.push_back(r[i].algo);
+    p->settled = false;
+    log_plan(*g, *p, M, N, K, "tuned");
+    return cs1_gemm(gemm, x, w, y, M, N, K, ldy, stream);
 }
 
 }  // extern "C"

@@ -27,6 +27,8 @@
 #include <cstring>
 #include <map>
 #include <new>
+#include <set>
+#include <tuple>
 #include <vector>
 
 #include "qwen3_5_model.h"
@@ -171,6 +173,8 @@ struct Model {
     Tensor embed, final_norm, lm_head;
     std::vector<Layer> layers;
     bool graph_enabled = false;
+    bool tune_gemm = false;                         // time hipBLASLt candidates per shape
+    std::set<std::tuple<int, int, int>> tuned;      // shapes (M, N, K) already tuned
     std::map<int, void*> graphs;  // prompt length -> executable graph
     int cos_len = 0;              // positions held by the rotary tables
     Prefix pre;
@@ -245,7 +249,18 @@ int rotary(Model& m) {
 }
 
 // y [T, N] = x [T, K] W^T with W [N, K]
+// (the first call at a shape re-chooses its plan by timing when tuning is on; never under
+// capture, where cs1_gemm keeps the deterministic plan)
 int gemm(Model& m, size_t x, const Tensor& wt, size_t y, int T, int N, int K) {
+    if (m.tune_gemm && T > 0 && !m.tuned.count({T, N, K})) {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        TRY(hipStreamIsCapturing(static_cast<hipStream_t>(m.stream), &cap));
+        if (cap == hipStreamCaptureStatusNone) {
+            TRY(cs1_gemm_tune(m.gemm, sc(m, x), at(m, wt), sc(m, y), T, N, K, N, m.stream));
+            m.tuned.insert({T, N, K});
+            return 0;
+        }
+    }
     return cs1_gemm(m.gemm, sc(m, x), at(m, wt), sc(m, y), T, N, K, N, m.stream);
 }
 
@@ -372,9 +387,14 @@ int run(Model& m, int T, Mode mode, const Cands* cd) {
     return 0;
 }
 
-int embed(Model& m, const int32_t* ids, int T) {
+bool ids_ok(const Model& m, const int32_t* ids, int T) {
     for (int t = 0; t < T; t++)
-        if (ids[t] < 0 || ids[t] >= m.cfg.vocab) return hipErrorInvalidValue;
+        if (ids[t] < 0 || ids[t] >= m.cfg.vocab) return false;
+    return true;
+}
+
+int embed(Model& m, const int32_t* ids, int T) {
+    if (!ids_ok(m, ids, T)) return hipErrorInvalidValue;
     TRY(cs1_upload(sc(m, m.s.ids), ids, (size_t)T * 4, m.stream));
     return cs1_embed(reinterpret_cast<const int32_t*>(sc(m, m.s.ids)), at(m, m.embed), sc(m, m.s.res), T,
                      m.cfg.hidden, m.stream);
@@ -430,7 +450,8 @@ void free_prefix(Prefix& p) {
 }
 
 int capture(Model& m, const int32_t* ids, int P) {
-    if (!ids || P < 64 || P % 64 != 0 || P > m.max_tokens) return hipErrorInvalidValue;
+    // every argument is checked before the previous prefix is released or any work is queued
+    if (!ids || P < 64 || P % 64 != 0 || P > m.max_tokens || !ids_ok(m, ids, P)) return hipErrorInvalidValue;
     free_prefix(m.pre);
     const Q35ModelConfig& c = m.cfg;
     Prefix& p = m.pre;
@@ -473,6 +494,7 @@ int score(Model& m, const int32_t* ids, const int32_t* lens, int n, double* scor
         R += lens[c];
         if (R > m.max_tokens) return hipErrorInvalidValue;
     }
+    if (!ids_ok(m, ids, R)) return hipErrorInvalidValue;
     std::vector<int> pos(R);
     for (int c = 0; c < n; c++)
         for (int j = 0; j < lens[c]; j++) pos[cd.off[c] + j] = P + j;
@@ -655,6 +677,12 @@ void q35m_destroy(void* model) {
 int q35m_set_graph(void* model, int enabled) {
     if (!model) return hipErrorInvalidValue;
     static_cast<Model*>(model)->graph_enabled = enabled != 0;
+    return 0;
+}
+
+int q35m_set_gemm_tuning(void* model, int enabled) {
+    if (!model) return hipErrorInvalidValue;
+    static_cast<Model*>(model)->tune_gemm = enabled != 0;
     return 0;
 }
 

@@ -80,10 +80,13 @@ ADDITIONS = {
     "cs1_gdn_conv_varlen": (_I, [P, _I, P, P, P, P, P, _I, P, _I, _I, P]),
     "cs1_attention_prefix_varlen": (_I, [P, P, P, _I, P, P, _I, _I, P, P, P, P, _I, _I, _I, _I, c_float, P]),
     "cs1_gdn_prefill_varlen": (_I, [P, P, P, P, P, P, P, P, _I, _I, _I, c_float, P, _SZ, P, _SZ, P]),
+    "cs1_gemm_tune": (_I, [P, P, P, P, _I, _I, _I, _I, P]),
 }
 
 HIP_ERROR_INVALID_VALUE = 1
 HIP_ERROR_NOT_SUPPORTED = 801
+HIP_ERROR_STREAM_CAPTURE_UNSUPPORTED = 900
+HIP_ERROR_STREAM_CAPTURE_INVALIDATED = 901
 
 
 class HipError(RuntimeError):

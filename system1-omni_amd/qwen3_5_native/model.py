@@ -20,7 +20,7 @@ GDN_IN, GDN_CONV, GDN_A_LOG, GDN_DT_BIAS, GDN_NORM, GDN_OUT = 4, 5, 6, 7, 8, 9
 ATTN_QKV, ATTN_Q_NORM, ATTN_K_NORM, ATTN_O = 10, 11, 12, 13
 MLP_GATE_UP, MLP_DOWN, LM_HEAD = 14, 15, 16
 
-SYMBOLS = ["q35m_create", "q35m_destroy", "q35m_set_graph", "q35m_forward", "q35m_decide", "q35m_capture",
+SYMBOLS = ["q35m_create", "q35m_destroy", "q35m_set_graph", "q35m_set_gemm_tuning", "q35m_forward", "q35m_decide", "q35m_capture",
            "q35m_score", "q35m_logprobs", "q35m_tensor", "q35m_stream"]
 
 
@@ -82,6 +82,7 @@ def load(path: str = None) -> ctypes.CDLL:
     lib.q35m_destroy.argtypes = [vp]
     lib.q35m_destroy.restype = None
     lib.q35m_set_graph.argtypes = [vp, ctypes.c_int]
+    lib.q35m_set_gemm_tuning.argtypes = [vp, ctypes.c_int]
     lib.q35m_forward.argtypes = [vp, i32p, ctypes.c_int, f32p]
     lib.q35m_decide.argtypes = [vp, i32p, ctypes.c_int, i32p, ctypes.c_int, f32p]
     lib.q35m_capture.argtypes = [vp, i32p, ctypes.c_int]
@@ -118,6 +119,9 @@ class Model:
 
     def set_graph(self, enabled: bool):
         hip.check(self.lib.q35m_set_graph(self.handle, int(enabled)), "q35m_set_graph")
+
+    def set_gemm_tuning(self, enabled: bool):
+        hip.check(self.lib.q35m_set_gemm_tuning(self.handle, int(enabled)), "q35m_set_gemm_tuning")
 
     def forward(self, ids) -> np.ndarray:
         ids = np.ascontiguousarray(ids, np.int32)

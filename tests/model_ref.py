@@ -3,27 +3,36 @@
 The op sequence is the reference executor's (src/models/qwen3_5/native/src/model.rs:1119-1318);
 each op is the oracle's emulation of the corresponding reference kernel, and each GEMM is the
 float64 product of the bf16 operands rounded once to bf16 (cuBLASLt / hipBLASLt accumulate
-in float32, so single results may differ by one bf16 step)."""
+in float32, so single results may differ by one bf16 step). For full-size models the GEMMs can
+run as float32 products (BLAS sgemm, float32 accumulation like the device's) rounded once to
+bf16, which keeps a 4B-class 4096-token forward within a minute or two of host time."""
+import functools
+
 import numpy as np
 
 import oracle as O
 from qwen3_5_native import model as QM
 
 
-def gemm(x, w, M, N, K):
-    xf = O.bf16_to_f32(x).reshape(M, K).astype(np.float64)
-    wf = O.bf16_to_f32(w).reshape(N, K).astype(np.float64)
-    return O.f32_to_bf16((xf @ wf.T).astype(np.float32)).reshape(-1)
+def gemm(x, w, M, N, K, fp32=False):
+    """fp32=False: float64 product; True: float32 BLAS product; either rounded once to bf16."""
+    xf = O.bf16_to_f32(x).reshape(M, K)
+    wf = O.bf16_to_f32(w).reshape(N, K)
+    if fp32:
+        return O.f32_to_bf16(np.ascontiguousarray(xf @ wf.T, np.float32)).reshape(-1)
+    return O.f32_to_bf16((xf.astype(np.float64) @ wf.T.astype(np.float64)).astype(np.float32)).reshape(-1)
 
 
-def forward(m: QM.Model, ids) -> np.ndarray:
+def forward(m: QM.Model, ids, fp32_gemm=False, progress=None) -> np.ndarray:
     """Final-norm hidden state of the last row, float."""
     T = len(ids)
-    return O.bf16_to_f32(forward_rows(m, ids).reshape(T, m.cfg.hidden)[T - 1])
+    return O.bf16_to_f32(forward_rows(m, ids, fp32_gemm, progress).reshape(T, m.cfg.hidden)[T - 1])
 
 
-def forward_rows(m: QM.Model, ids) -> np.ndarray:
-    """Final-norm hidden states of every row, bf16 bits [T * hidden]."""
+def forward_rows(m: QM.Model, ids, fp32_gemm=False, progress=None) -> np.ndarray:
+    """Final-norm hidden states of every row, bf16 bits [T * hidden]. progress(i), if given,
+    is called after each layer."""
+    gemm_ = functools.partial(gemm, fp32=fp32_gemm)
     c = m.cfg
     T = len(ids)
     kd, vd = c.lin_k_heads * c.lin_k_dim, c.lin_v_heads * c.lin_v_dim
@@ -38,7 +47,7 @@ def forward_rows(m: QM.Model, ids) -> np.ndarray:
     x = O.rms_norm(res, m.tensor(QM.INPUT_NORM, 0), T, H, c.eps)
     for i in range(c.layers):
         if not c.is_full(i):
-            gi = gemm(x, m.tensor(QM.GDN_IN, i), T, gdn_w, H)
+            gi = gemm_(x, m.tensor(QM.GDN_IN, i), T, gdn_w, H)
             q, k, v = O.gdn_conv(gi, gdn_w, m.tensor(QM.GDN_CONV, i), T, kd, vd)
             beta, g = O.gdn_gates(gi[conv + vd:], gi[conv + vd + c.lin_v_heads:], gdn_w, m.tensor(QM.GDN_A_LOG, i),
                                   m.tensor(QM.GDN_DT_BIAS, i), T, c.lin_v_heads)
@@ -46,21 +55,23 @@ def forward_rows(m: QM.Model, ids) -> np.ndarray:
                                     c.lin_v_heads, c.lin_k_heads, scale=c.lin_k_dim ** -0.5, want_state=False)
             ln = O.gated_rms_norm(o.reshape(-1), gi[conv:], gdn_w, m.tensor(QM.GDN_NORM, i), T, c.lin_v_heads,
                                   c.lin_v_dim, c.eps)
-            delta = gemm(ln, m.tensor(QM.GDN_OUT, i), T, H, vd)
+            delta = gemm_(ln, m.tensor(QM.GDN_OUT, i), T, H, vd)
         else:
-            ai = gemm(x, m.tensor(QM.ATTN_QKV, i), T, attn_w, H)
+            ai = gemm_(x, m.tensor(QM.ATTN_QKV, i), T, attn_w, H)
             q, gate, k = O.attn_prep(ai, ai[attn_q:], attn_w, m.tensor(QM.ATTN_Q_NORM, i),
                                      m.tensor(QM.ATTN_K_NORM, i), cs, sn, T, c.heads, c.kv_heads, D,
                                      c.rotary_half, c.eps)
             ao = O.attention_emul(q.reshape(-1), k.reshape(-1), ai[attn_q + c.kv_heads * D:], attn_w,
                                   gate.reshape(-1), T, c.heads, c.kv_heads, D, D ** -0.5)
-            delta = gemm(ao.reshape(-1), m.tensor(QM.ATTN_O, i), T, H, c.heads * D)
+            delta = gemm_(ao.reshape(-1), m.tensor(QM.ATTN_O, i), T, H, c.heads * D)
         res, x = O.add_rms_norm(res, delta, m.tensor(QM.POST_NORM, i), T, H, c.eps)
-        gu = gemm(x, m.tensor(QM.MLP_GATE_UP, i), T, 2 * I, H)
+        gu = gemm_(x, m.tensor(QM.MLP_GATE_UP, i), T, 2 * I, H)
         act = O.silu_mul(gu, 2 * I, T, I)
-        delta = gemm(act.reshape(-1), m.tensor(QM.MLP_DOWN, i), T, H, I)
+        delta = gemm_(act.reshape(-1), m.tensor(QM.MLP_DOWN, i), T, H, I)
         nxt = m.tensor(QM.INPUT_NORM, i + 1) if i + 1 < c.layers else m.tensor(QM.FINAL_NORM)
         res, x = O.add_rms_norm(res, delta, nxt, T, H, c.eps)
+        if progress is not None:
+            progress(i)
     return np.asarray(x).reshape(-1)
 
 

@@ -76,10 +76,11 @@ def test_gdn_conv_continuation_uses_cached_history():
             assert not np.array_equal(missing[i][:m], want[:m])
 
 
-def test_gdn_gates_match_emulator():
+@pytest.mark.parametrize("T,H,ld", [(4096, 32, 2 * 32 + 40), (8192, 48, 96), (77, 6, 13), (1, 8, 9)])
+def test_gdn_gates_match_emulator(T, H, ld):
+    """Vector path (H % 8 == 0, ld % 8 == 0) and the any-shape path (odd H or ld)."""
     api, st = hip.api(), stream()
-    T, H, ld = 4096, 32, 2 * 32 + 40
-    say("gdn_gates")
+    say(f"gdn_gates T={T} H={H} ld={ld}")
     rng = np.random.default_rng(3)
     b = O.f32_to_bf16((rng.standard_normal(T * ld) * 3).astype(np.float32))
     a = O.f32_to_bf16((rng.standard_normal(T * ld) * 8).astype(np.float32))

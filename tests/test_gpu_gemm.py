@@ -79,27 +79,33 @@ def test_gemm_edge_arguments(gemm):
     assert api.cs1_gemm(None, None, None, None, 4, 16, 16, 16, st.handle) == hip.HIP_ERROR_INVALID_VALUE
 
 
-def test_gemm_tuned_and_untuned_plans_agree(monkeypatch):
-    """A plan tuned on first use (the fastest of hipBLASLt's heuristic candidates) and the
-    first heuristic choice (CS1_GEMM_TUNE=0) both stay within one bf16 step of the float64
-    product, and each is bitwise repeatable once built. The shape is one of the 27B-class
-    candidate-scoring projections, where the measured choice differs from the first."""
-    api = hip.api()
+def test_gemm_tuned_and_default_plans_agree():
+    """cs1_gemm_tune (the fastest of hipBLASLt's heuristic candidates, timed on these
+    operands) and the default plan (the first heuristic choice without atomic split-K) both
+    stay within one bf16 step of the float64 product, and each is bitwise repeatable once
+    built. The shape is one of the 27B-class candidate-scoring projections, where the
+    measured choice differs from the first."""
+    api, st = hip.api(), stream()
     M, N, K = 1217, 5120, 6144
-    say(f"gemm tuned vs untuned M={M} N={N} K={K}")
+    say(f"gemm tuned vs default M={M} N={N} K={K}")
     rng = np.random.default_rng(11)
     x = O.f32_to_bf16(rng.standard_normal(M * K).astype(np.float32))
     w = O.f32_to_bf16((rng.standard_normal(N * K) * 0.02).astype(np.float32))
     want = ref(x, w, M, N, K)
     mask = np.abs(O.bf16_to_f32(want)) > 1e-2 * np.abs(O.bf16_to_f32(want)).max()
     outs = []
-    for tune in ("1", "0"):
-        monkeypatch.setenv("CS1_GEMM_TUNE", tune)
+    for tune in (True, False):
         h = api.cs1_gemm_create(32 << 20)
         assert h
         try:
+            if tune:
+                dx, dw, y = dev(x), dev(w), empty(M * N * 2)
+                hip.check(api.cs1_gemm_tune(h, dx.at(0), dw.at(0), y.at(0), M, N, K, N, st.handle), "gemm tune")
+                tuned_out = get_bf16(y, M * N).reshape(M, N)
             a = run(h, x, w, M, N, K)
             np.testing.assert_array_equal(a, run(h, x, w, M, N, K))
+            if tune:
+                np.testing.assert_array_equal(a, tuned_out)
         finally:
             api.cs1_gemm_destroy(h)
         say(f"  tune={tune}: ulp vs float64 {ulp_diff(a[mask], want[mask])}")
@@ -108,10 +114,64 @@ def test_gemm_tuned_and_untuned_plans_agree(monkeypatch):
     assert ulp_diff(outs[0][mask], outs[1][mask]) <= 1
 
 
-def test_gemm_plan_first_built_under_capture(monkeypatch):
-    """A shape whose first call is recorded into a HIP graph cannot be timed; its plan takes
-    hipBLASLt's first heuristic choice, so every replay equals an eager call of an untuned
-    handle bit for bit (with eager work on the stream between the replays)."""
+def test_gemm_default_plan_is_the_same_in_every_handle():
+    """Without tuning, a shape's plan does not depend on the handle or on timing: two fresh
+    handles give bitwise identical results (what makes model outputs repeatable from one
+    process to the next)."""
+    api = hip.api()
+    M, N, K = 1217, 17408 // 8, 5120
+    say(f"gemm default plan in two handles M={M} N={N} K={K}")
+    rng = np.random.default_rng(12)
+    x = O.f32_to_bf16(rng.standard_normal(M * K).astype(np.float32))
+    w = O.f32_to_bf16((rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    outs = []
+    for _ in range(2):
+        h = api.cs1_gemm_create(32 << 20)
+        assert h
+        try:
+            outs.append(run(h, x, w, M, N, K))
+        finally:
+            api.cs1_gemm_destroy(h)
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+def test_gemm_tune_refused_under_capture():
+    """cs1_gemm_tune waits on the host, so under stream capture it refuses with
+    hipErrorStreamCaptureUnsupported and records nothing; the capture then still ends and
+    replays a plain cs1_gemm."""
+    api, st = hip.api(), stream()
+    M, N, K = 64, 256, 256
+    say("gemm tune under capture")
+    rng = np.random.default_rng(3)
+    x = O.f32_to_bf16(rng.standard_normal(M * K).astype(np.float32))
+    w = O.f32_to_bf16((rng.standard_normal(N * K) * 0.05).astype(np.float32))
+    dx, dw, y = dev(x), dev(w), empty(M * N * 2)
+    h = api.cs1_gemm_create(32 << 20)
+    assert h
+    codes = []
+    graph = None
+    try:
+        def body():
+            codes.append(api.cs1_gemm_tune(h, dx.at(0), dw.at(0), y.at(0), M, N, K, N, st.handle))
+            hip.check(api.cs1_gemm(h, dx.at(0), dw.at(0), y.at(0), M, N, K, N, st.handle), "gemm")
+        graph = hip.Graph(st, body)
+        graph.launch(st)
+        got = get_bf16(y, M * N).reshape(M, N)
+    finally:
+        graph = None
+        api.cs1_gemm_destroy(h)
+    assert codes == [hip.HIP_ERROR_STREAM_CAPTURE_UNSUPPORTED]
+    h0 = api.cs1_gemm_create(32 << 20)
+    try:
+        np.testing.assert_array_equal(got, run(h0, x, w, M, N, K))
+    finally:
+        api.cs1_gemm_destroy(h0)
+
+
+def test_gemm_plan_first_built_under_capture():
+    """A shape whose first call is recorded into a HIP graph gets the same deterministic
+    plan as an eager call, so every replay equals an eager call of a fresh handle bit for
+    bit (with eager work on the stream between the replays)."""
     api, st = hip.api(), stream()
     M, N, K = 96, 384, 640
     say(f"gemm plan built under capture M={M} N={N} K={K}")
@@ -119,7 +179,6 @@ def test_gemm_plan_first_built_under_capture(monkeypatch):
     x = O.f32_to_bf16(rng.standard_normal(M * K).astype(np.float32))
     w = O.f32_to_bf16((rng.standard_normal(N * K) * 0.05).astype(np.float32))
     dx, dw, y = dev(x), dev(w), empty(M * N * 2)
-    monkeypatch.setenv("CS1_GEMM_TUNE", "1")
     h = api.cs1_gemm_create(32 << 20)
     assert h
     graph = None
@@ -135,7 +194,6 @@ def test_gemm_plan_first_built_under_capture(monkeypatch):
     finally:
         graph = None
         api.cs1_gemm_destroy(h)
-    monkeypatch.setenv("CS1_GEMM_TUNE", "0")
     h0 = api.cs1_gemm_create(32 << 20)
     assert h0
     try:
