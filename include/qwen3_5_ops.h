@@ -202,6 +202,17 @@ int cs1_attention_prefix_varlen(const void* q, const void* k, const void* v, int
                                 int ldvp, int pre, const void* gate, void* out, float* lse, const int32_t* cu_seqlens,
                                 int nseq, int Hq, int Hk, int Dh, float scale, void* stream);
 
+/* No counterpart in the reference: cs1_gdn_prefill_x without the workspace argument, for
+ * callers that cannot allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The workspace is a 64 MiB array inside the library, one
+ * per GPU, kept until the process ends; the call itself allocates nothing.  Limit: the
+ * workspace of (T, H) must fit, i.e. ceil(T / 64) * H <= 910 (e.g. T <= 1792 at H = 32,
+ * T <= 58,240 at H = 1); larger shapes return hipErrorInvalidValue.  Every call on a GPU
+ * shares that GPU's array, so calls that overlap in time on one GPU race: serialise them.
+ * Results are bit for bit those of cs1_gdn_prefill_x. */
+int cs1_gdn_prefill_x_static(const void* q, const void* k, const void* v, const float* g, const void* beta, void* o,
+                             int T, int H, int HK, float scale, const void* s_in, void* s_out, void* stream);
+
 /* Varlen form of cs1_gdn_prefill_x for packed sequences (the candidate-packed prefill of the
  * reference's scoring path, model.rs:1421-1470, which runs the delta rule per candidate):
  * cu_seqlens is a HOST array of nseq + 1 (at most 64) nondecreasing row offsets with

@@ -36,6 +36,8 @@
 //     bf16(S) and v_new through LDS.  The output o = qd Sb + pb v_new is produced in the
 //     same pass, so per-chunk states and v_new never go to memory.  The slices of one head
 //     run on the same XCD (block = slice * H + head) and share its L2.
+#include <mutex>
+
 #include "common.h"
 
 namespace q35 {
@@ -779,6 +781,53 @@ extern "C" int cs1_gdn_prefill_x(const void* q, const void* k, const void* v, co
                                  void* o, float* workspace, int T, int H, int HK, float scale, const void* s_in,
                                  void* s_out, void* stream) {
     return gdn_run(q, k, v, g, beta, o, workspace, T, H, HK, scale, s_in, 0, s_out, 0, GSeqs{0, {}, {}}, stream);
+}
+
+// ---- cs1_gdn_prefill_x_static: the same launch pair with a library-owned workspace ----
+//
+// For callers that cannot allocate (code under graph capture, tight serving loops): the
+// workspace is this file-scope device array, one copy per GPU, held until the process ends.
+// Host code never passes `scratch` itself to a kernel (its host-side name is only a stand-in
+// for the symbol); it passes the device address that hipGetSymbolAddress returns, looked up
+// once per device with that device current. The prep kernel writes every workspace byte the
+// scan reads, so nothing has to be cleared between calls. Calls that overlap on one GPU share
+// the array and race; a caller serialises them (one stream, or events).
+constexpr size_t STATIC_SCRATCH_BYTES = (size_t)64 << 20;
+__device__ __align__(256) unsigned char scratch[STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[MAX_DEVICES];
+
+// The current device's address of `scratch`, looked up on the first call on that device.
+hipError_t device_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        scratch_ptr[dev] = p;
+    }
+    *out = scratch_ptr[dev];
+    return hipSuccess;
+}
+}  // namespace
+
+extern "C" int cs1_gdn_prefill_x_static(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                                        void* o, int T, int H, int HK, float scale, const void* s_in, void* s_out,
+                                        void* stream) {
+    if (T < 0 || H <= 0) return hipErrorInvalidValue;
+    if (Layout((size_t)((T + C - 1) / C), H).total > STATIC_SCRATCH_BYTES) return hipErrorInvalidValue;
+    void* ws = nullptr;
+    const hipError_t e = device_scratch(&ws);
+    if (e != hipSuccess) return e;
+    return gdn_run(q, k, v, g, beta, o, static_cast<float*>(ws), T, H, HK, scale, s_in, 0, s_out, 0,
+                   GSeqs{0, {}, {}}, stream);
 }
 
 extern "C" int cs1_gdn_prefill_varlen(const void* q, const void* k, const void* v, const float* g, const void* beta,

@@ -81,6 +81,7 @@ ADDITIONS = {
     "cs1_attention_prefix_varlen": (_I, [P, P, P, _I, P, P, _I, _I, P, P, P, P, _I, _I, _I, _I, c_float, P]),
     "cs1_gdn_prefill_varlen": (_I, [P, P, P, P, P, P, P, P, _I, _I, _I, c_float, P, _SZ, P, _SZ, P]),
     "cs1_gemm_tune": (_I, [P, P, P, P, _I, _I, _I, _I, P]),
+    "cs1_gdn_prefill_x_static": (_I, [P, P, P, P, P, P, _I, _I, _I, c_float, P, P, P]),
 }
 
 HIP_ERROR_INVALID_VALUE = 1
