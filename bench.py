@@ -319,6 +319,28 @@ def bench_hbm_ops(api, st, ev, steps, warmup):
           lambda: hip.check(api.cs1_attn_prep(row.at(0), row.at(Hq * 2 * Dh * 2), ld, qw.at(0), kw.at(0), cs.at(0),
                                               sn.at(0), q.at(0), gate.at(0), k.at(0), T, Hq, Hk, Dh, half, 1e-6,
                                               st.handle), "attn prep"))
+    # the decoder glue of config 3 (T=4096, hidden 2560, SwiGLU 9728): residual norms, SwiGLU,
+    # embedding gather (norm.cu:11-73, elementwise.cu:11-16, 75-87)
+    T, Dm, I = 4096, 2560, 9728
+    xr = hip.to_device(bf16(rng, T * Dm), st)
+    dl = hip.to_device(bf16(rng, T * Dm), st)
+    wn = hip.to_device(bf16(rng, Dm, 0.1), st)
+    on = hip.DeviceBuffer(T * Dm * 2)
+    entry("rms_norm", "cfg3 RMSNorm T=4096 D=2560", 2 * T * Dm * 2,
+          lambda: hip.check(api.cs1_rms_norm(xr.at(0), wn.at(0), on.at(0), T, Dm, 1e-6, st.handle), "rms norm"))
+    # the residual is updated in place: every launch reads and writes it (values drift, bytes do not)
+    entry("add_rms_norm", "cfg3 residual add + RMSNorm T=4096 D=2560", 4 * T * Dm * 2,
+          lambda: hip.check(api.cs1_add_rms_norm(xr.at(0), dl.at(0), wn.at(0), on.at(0), T, Dm, 1e-6, st.handle),
+                            "add rms norm"))
+    gu = hip.to_device(bf16(rng, T * 2 * I), st)
+    act = hip.DeviceBuffer(T * I * 2)
+    entry("silu_mul", "cfg3 SwiGLU T=4096 I=9728", 3 * T * I * 2,
+          lambda: hip.check(api.cs1_silu_mul(gu.at(0), 2 * I, act.at(0), T, I, st.handle), "silu mul"))
+    V = 151936
+    table = hip.to_device(bf16(rng, V * Dm, 0.02), st)
+    ids = hip.to_device(rng.integers(0, V, T).astype(np.int32), st)
+    entry("embed", "cfg3 embedding gather T=4096 D=2560 vocab 151936", 2 * T * Dm * 2 + T * 4,
+          lambda: hip.check(api.cs1_embed(ids.at(0), table.at(0), on.at(0), T, Dm, st.handle), "embed"))
     return res
 
 

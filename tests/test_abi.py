@@ -45,9 +45,14 @@ def test_workspace_size_is_pure_and_monotone(api):
     a = api.cs1_gdn_workspace_floats(64, 4)
     assert a == api.cs1_gdn_workspace_floats(1, 4) > 0
     assert api.cs1_gdn_workspace_floats(65, 4) > a
-    # per (head, chunk): w, u, qd, kd^T (64x128 bf16) + pb (64x64 bf16) + decay, 256-B aligned parts
+    # per (head, chunk): w, u, qd, kd^T (64x128 bf16) + pb (64x64 bf16) + decay, 256-B aligned parts;
+    # a sequence long enough to run in segments (records > 150 MiB) adds two float32 states
+    rec = 4 * 64 * 128 * 2 + 64 * 64 * 2
+    mid = api.cs1_gdn_workspace_floats(4096, 32) * 4
+    assert 32 * 64 * rec <= mid < 32 * 64 * (rec + 4) + 4096
     big = api.cs1_gdn_workspace_floats(8192, 32) * 4
-    assert 32 * 128 * (4 * 64 * 128 * 2 + 64 * 64 * 2) <= big < 32 * 128 * (4 * 64 * 128 * 2 + 64 * 64 * 2 + 4) + 4096
+    states = 2 * 32 * 128 * 128 * 4
+    assert 32 * 128 * rec + states <= big < 32 * 128 * (rec + 4) + 4096 + states
 
 
 def test_argument_errors_and_empty_work(api):
