@@ -889,6 +889,315 @@ int launch_flash32(const void* q, const void* k, const void* v, int ldv, const v
                                                         st);
 }
 
+// flash256_kernel: the Dh = 256 path (q heads per kv head even) on the 32x32x16 MFMA, built
+// like flash32_kernel. A block owns 64 rows of one q-head pair; its eight waves are 4 row
+// quarters x 2 dim halves, and a wave owns 16 query rows of the pair (32 query columns) and
+// one half of the 256 dims. Per 32-key tile a wave computes its half of S^T = K Q^T (8 MFMAs
+// over its 128 dims), the two waves of a dim pair exchange those partial scores through LDS
+// and both add them in the same order (dims 0-127 first), so they hold identical scores,
+// softmax statistics and P; each then accumulates O^T += V^T P^T for its own 128 dims. Every
+// K/V tile in LDS serves 128 query columns. Tiles move global -> LDS by buffer_load ... lds
+// with flash32's chunk permutations (K: c ^ (r & 15), V: c ^ f(r & 3)) through three stages
+// (K two steps ahead, V one), and the partial scores alternate between two exchange buffers,
+// so a step needs one barrier. Tile boundaries are fixed multiples of 32 from key 0, so a row's
+// arithmetic does not depend on its block (windowed and packed launches repeat the full pass
+// bit for bit).
+namespace fa256 {
+constexpr int BN = 32;                     // keys per tile
+constexpr int ROWS = 64;                   // query rows per block
+constexpr int NSTAGE = 3;                  // K two steps ahead, V one
+constexpr int ROW = 512;                   // bytes per K or V row (256 bf16)
+constexpr int K_BYTES = BN * ROW;          // 16384
+constexpr int STAGE = 2 * K_BYTES;
+constexpr int XCH = 8 * 4096;              // one partial-score tile per wave
+constexpr int BYTES = NSTAGE * STAGE + 2 * XCH;  // the stages and two exchange buffers (160 KB)
+// at most one step of transfers (four per wave) outstanding before a step's barrier
+constexpr int VMCNT_ONE_STEP = 0x0f74;
+}  // namespace fa256
+
+template <bool GATED, bool PREFIX>
+__global__ void __launch_bounds__(512, 1)
+    flash256_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, int ldv,
+                    const bf16* __restrict__ gate, bf16* __restrict__ out, float* __restrict__ lse, int T, int Hq,
+                    int Hk, float scale_log2, int q_base, const Seqs seqs) {
+    using namespace fa256;
+    using fa32::k_slot;
+    using fa32::v_slot;
+    using fa32::mfma32;
+    using fa32::max_halves;
+    using fa32::read_tr;
+    using fa32::dma16;
+    constexpr int D = 256;
+    int b = blockIdx.x, lse_ld = T;
+    if (seqs.n > 0) {
+        int sq = 0;
+        while (sq + 1 < seqs.n && b >= seqs.blk[sq + 1]) sq++;
+        b -= seqs.blk[sq];
+        // rows are addressed by position: position P + i is the sequence's row i
+        const int r0 = seqs.cu[sq], P = seqs.pre;
+        T = seqs.cu[sq + 1] - r0 + P;
+        q_base = P;
+        lse_ld = seqs.lse_ld;
+        const ptrdiff_t sh = (ptrdiff_t)r0 - P;
+        q += sh * Hq * D;
+        k += sh * Hk * D;
+        v += sh * ldv;
+        if (GATED) gate += sh * Hq * D;
+        out += sh * Hq * D;
+        if (lse != nullptr) lse += sh;
+    }
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // wave = 2 rq + dh: row quarter rq, dim half dh
+    const int rq = __builtin_amdgcn_readfirstlane(wave >> 1), dh = __builtin_amdgcn_readfirstlane(wave & 1);
+    const int c32 = lane & 31, hh = lane >> 5;  // query column, lane half
+    const int units = Hq / 2;
+    const int nblk = (T - q_base + ROWS - 1) / ROWS;
+    const int unit = b % units;
+    const int q0 = q_base + (nblk - 1 - b / units) * ROWS;  // longest blocks first
+    const int hk = unit * 2 / (Hq / Hk);
+    const int h = unit * 2 + (c32 >> 4);           // this lane's q head
+    const int qrow = q0 + 16 * rq + (c32 & 15);    // this lane's query row
+    const int wq0 = q0 + 16 * rq;                   // this wave's first query row
+    const bf16* kh = k + (size_t)hk * D;
+    const bf16* vh = v + (size_t)hk * D;
+    const int ldk = Hk * D;
+
+    const int kv_end = min(T, q0 + ROWS);
+    const int ntiles = (kv_end + BN - 1) / BN;
+    auto lds_addr = [&](const unsigned char* p) {
+        return (uint32_t)__builtin_amdgcn_readfirstlane(
+            (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char*)p);
+    };
+    // DMA: wave w moves rows 4 w .. 4 w + 3 of a K or V tile as two 1 KB instructions of two
+    // rows each; lane l fills slot l % 32 of row l / 32 with the chunk that belongs there
+    const int drow = lane >> 5, dslot = lane & 31;
+    int kvoff[2], vvoff[2], vvoff_p[2];
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        const int r = 4 * wave + 2 * n + drow;
+        kvoff[n] = drow * ldk * 2 + (k_slot(r, dslot) << 4);
+        vvoff[n] = drow * ldv * 2 + (v_slot(r, dslot) << 4);
+        vvoff_p[n] = drow * seqs.ldvp * 2 + (v_slot(r, dslot) << 4);
+    }
+    const uint32_t gbase = lds_addr(smem);
+    const bf16* kph = seqs.kp + (size_t)hk * D;
+    const bf16* vph = seqs.vp + (size_t)hk * D;
+    auto rsrc = [&](const bf16* base, int ld, int k0, int lim, bool valid) {
+        const uint64_t a = (uint64_t)(base + (size_t)k0 * ld);
+        const int rows = valid ? min(lim - k0, BN) : 0;
+        const int bytes = rows > 0 ? ((rows - 1) * ld + D) * 2 : 0;
+        return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                     (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) & 0xffffu,
+                     (uint32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000u};
+    };
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);
+    auto dma_tile = [&](const u32x4& r, uint32_t dst, int ld, const int* voff) {
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            const int row0 = 4 * uwave + 2 * n;
+            dma16(r, dst + row0 * ROW, voff[n], row0 * ld * 2);
+        }
+    };
+    auto dma_k = [&](int j, int sidx, bool valid) {
+        const int k0 = j * BN;
+        if (PREFIX && k0 < seqs.pre)
+            dma_tile(rsrc(kph, ldk, k0, seqs.pre, valid), gbase + sidx * STAGE, ldk, kvoff);
+        else
+            dma_tile(rsrc(kh, ldk, k0, T, valid), gbase + sidx * STAGE, ldk, kvoff);
+    };
+    auto dma_v = [&](int j, int sidx, bool valid) {
+        const int k0 = j * BN;
+        if (PREFIX && k0 < seqs.pre)
+            dma_tile(rsrc(vph, seqs.ldvp, k0, seqs.pre, valid), gbase + sidx * STAGE + K_BYTES, seqs.ldvp, vvoff_p);
+        else
+            dma_tile(rsrc(vh, ldv, k0, T, valid), gbase + sidx * STAGE + K_BYTES, ldv, vvoff);
+    };
+
+    // Pipeline prologue: K(0) and an empty V(-1), the Q fragments, then K(1) and V(0).
+    dma_k(0, 0, ntiles > 0);
+    dma_v(-1, 2, false);
+    // Q^T (B operand): column c32, dims 128 dh + 16 s + 8 hh .. + 7 (this wave's half)
+    u32x4 qf[8];
+    {
+        const bf16* qr = q + ((size_t)min(qrow, T - 1) * Hq + h) * D + 128 * dh + 8 * hh;
+#pragma unroll
+        for (int s = 0; s < 8; s++) qf[s] = ldg16(qr + 16 * s);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) asm volatile("" ::"v"(qf[i]));
+    wait_vm_all();
+    dma_k(1, 1, ntiles > 1);
+    dma_v(0, 0, ntiles > 0);
+    __syncthreads();
+
+    f32x16 o[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[t][i] = 0.f;
+    float m = -INFINITY, l = 0.f;
+
+    const int kf = c32 * ROW;
+    const int gi = lane & 15, gg = lane >> 4;
+    const int vrow = 4 * (gg >> 1) + (gi >> 2);                 // + 16 s + 8 e
+    const int vdim = 128 * dh + 16 * (gg & 1) + 4 * (gi & 3);   // + 32 t
+    auto vt = [&](int t, int s, int e) {
+        const int r = 16 * s + 8 * e + vrow, dim = 32 * t + vdim;
+        return r * ROW + (v_slot(r, dim >> 3) << 4) + 2 * (dim & 7);
+    };
+
+    // Partial scores are exchanged through LDS: buffer it % 2, 4 KB per wave, holds a wave's
+    // partial S of tile it as [4][64 lanes] x 16 bytes. A partner reads tile it's partial in
+    // step it + 1, and the buffer is rewritten in step it + 2, after that step's barrier.
+    unsigned char* const xch = smem + NSTAGE * STAGE;
+    unsigned char* const xown = xch + wave * 4096 + lane * 16;
+    const unsigned char* const xpart = xch + (wave ^ 1) * 4096 + lane * 16;
+    f32x16 sp;  // this wave's partial scores of the tile whose softmax is pending
+#pragma unroll
+    for (int i = 0; i < 16; i++) sp[i] = 0.f;
+    // sc = it % 3
+    auto step = [&](int it, int sc, bool may_mask) {
+        const unsigned char* kb = smem + sc * STAGE;
+        const unsigned char* vb = smem + (sc == 0 ? 2 : sc - 1) * STAGE + K_BYTES;
+        const int xr = ((it + 1) & 1) * XCH, xw = (it & 1) * XCH;
+        u32x4 kfr[8], vfr[2][2];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            kfr[ks] = *reinterpret_cast<const u32x4*>(kb + kf + (k_slot(c32, 16 * dh + 2 * ks + hh) << 4));
+        // the partner's partial scores of tile it - 1 (step 0: of the empty tile, whose scores
+        // are masked below)
+        f32x16 s;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(xpart + xr + j * 1024);
+#pragma unroll
+            for (int e = 0; e < 4; e++) s[4 * j + e] = x[e];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        dma_k(it + 2, sc == 0 ? 2 : sc - 1, it + 2 < ntiles);
+        __builtin_amdgcn_sched_barrier(0);
+        // QK^T of tile it over this wave's dims
+        f32x16 sn;
+#pragma unroll
+        for (int i = 0; i < 16; i++) sn[i] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) sn = mfma32(kfr[ks], qf[ks], sn);
+        // full scores of tile it - 1 (the same order in both waves of the pair: dims 0-127
+        // first), then the softmax statistics: s[i] is key k0 + 8 (i / 4) + 4 hh + i % 4
+        s = dh == 0 ? sp + s : s + sp;
+        const int k0 = (it - 1) * BN;
+        if (it == 0 || (may_mask && (k0 + BN - 1 > wq0 || k0 + BN > T))) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int key = k0 + 8 * (i >> 2) + 4 * hh + (i & 3);
+                if (it == 0 || key > qrow || key >= T) s[i] = -INFINITY;
+            }
+        }
+        float mx = s[0];
+#pragma unroll
+        for (int i = 1; i < 16; i++) mx = fmaxf(mx, s[i]);
+        mx = max_halves(mx) * scale_log2;
+        if (!__all(mx <= m + fa32::RESCALE_SLACK)) {
+            const float mn = fmaxf(m, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m - (mn == -INFINITY ? 0.f : mn));
+            m = mn;
+            l *= alpha;
+#pragma unroll
+            for (int t = 0; t < 4; t++) o[t] *= alpha;
+        }
+        const float base = m == -INFINITY ? 0.f : m;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            s[i] = __builtin_amdgcn_exp2f(fmaf(s[i], scale_log2, -base));
+            l += s[i];
+        }
+        u32x4 pf[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            pf[j] = u32x4{pack2(s[8 * j], s[8 * j + 1]), pack2(s[8 * j + 2], s[8 * j + 3]),
+                          pack2(s[8 * j + 4], s[8 * j + 5]), pack2(s[8 * j + 6], s[8 * j + 7])};
+        // publish this wave's partial of tile it
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *reinterpret_cast<f32x4*>(xown + xw + j * 1024) =
+                f32x4{sn[4 * j], sn[4 * j + 1], sn[4 * j + 2], sn[4 * j + 3]};
+        sp = sn;
+        __builtin_amdgcn_sched_barrier(0);
+        dma_v(it + 1, sc == 2 ? 0 : sc + 1, it + 1 < ntiles);
+        __builtin_amdgcn_sched_barrier(0);
+        // P V for this wave's 128 dims, V^T fragments read per dim tile
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const u32x2 lo = read_tr(vb + vt(t, j, 0)), hi = read_tr(vb + vt(t, j, 1));
+                vfr[t & 1][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) o[t] = mfma32(vfr[t & 1][j], pf[j], o[t]);
+        }
+        __builtin_amdgcn_s_waitcnt(VMCNT_ONE_STEP);
+        __syncthreads();
+    };
+    // Steps 0 .. n_main - 1 see no masked tile (tiles 0 .. ulast lie wholly below this wave's
+    // first row and below T); every wave runs ntiles + 1 steps in all.
+    const int lim = min(wq0 + 1, T) - BN;
+    const int ulast = lim >= 0 ? lim / BN : -1;  // last unmasked tile index
+    const int n_main = ulast >= 0 ? ulast + 2 : 1;
+    int it = 0, sc = 0;
+    for (; it < n_main; it++, sc = sc == 2 ? 0 : sc + 1) step(it, sc, false);
+    for (; it <= ntiles; it++, sc = sc == 2 ? 0 : sc + 1) step(it, sc, true);
+    wait_vm_all();
+
+    // o[t][i]: dim 128 dh + 32 t + 8 (i / 4) + 4 hh + i % 4 of query column c32
+    if (qrow >= T) return;
+    const float lt = l + __shfl_xor(l, 32, 64);
+    const float inv = 1.f / lt;
+    const size_t orow = ((size_t)qrow * Hq + h) * D + 128 * dh + 4 * hh;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int off = 32 * t + 8 * j;
+            float a[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) a[r] = o[t][4 * j + r] * inv;
+            if (GATED) {
+                const u32x2 gp = *reinterpret_cast<const u32x2*>(gate + orow + off);
+                a[0] = round_bf16(a[0]) * round_bf16(gate_sigmoid(lo_f32(gp[0])));
+                a[1] = round_bf16(a[1]) * round_bf16(gate_sigmoid(hi_f32(gp[0])));
+                a[2] = round_bf16(a[2]) * round_bf16(gate_sigmoid(lo_f32(gp[1])));
+                a[3] = round_bf16(a[3]) * round_bf16(gate_sigmoid(hi_f32(gp[1])));
+            }
+            *reinterpret_cast<u32x2*>(out + orow + off) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
+        }
+    if (lse != nullptr && dh == 0 && hh == 0) lse[(size_t)h * lse_ld + qrow] = (m + log2f(lt)) * 0.69314718055994531f;
+}
+
+template <bool GATED, bool PREFIX>
+int launch_flash256_as(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse,
+                       int T, int Hq, int Hk, float scale, int q_base, int blocks, const Seqs& sq, hipStream_t st) {
+    static const hipError_t configured =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(flash256_kernel<GATED, PREFIX>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, fa256::BYTES);
+    if (configured != hipSuccess) return configured;
+    flash256_kernel<GATED, PREFIX><<<blocks, 512, fa256::BYTES, st>>>(
+        static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
+        static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, T, Hq, Hk, scale * 1.4426950408889634f, q_base,
+        sq);
+    return hipGetLastError();
+}
+
+template <bool GATED>
+int launch_flash256(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse,
+                    int T, int Hq, int Hk, float scale, int q_base, int blocks, const Seqs& sq, hipStream_t st) {
+    return sq.pre > 0
+               ? launch_flash256_as<GATED, true>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, blocks, sq, st)
+               : launch_flash256_as<GATED, false>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base, blocks, sq,
+                                                  st);
+}
+
 template <int D, bool GATED, bool GQA4>
 int launch_flash(const void* q, const void* k, const void* v, int ldv, const void* gate, void* out, float* lse, int T,
                  int Hq, int Hk, float scale, int q_base, hipStream_t st) {
@@ -907,6 +1216,9 @@ int launch_flash(const void* q, const void* k, const void* v, int ldv, const voi
     if (D == 128 && GQA4)
         return launch_flash32<GATED>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base,
                                      (T - q_base + fa32::ROWS - 1) / fa32::ROWS * (Hq / 4), one, st);
+    if (D == 256 && (Hq / Hk) % 2 == 0)
+        return launch_flash256<GATED>(q, k, v, ldv, gate, out, lse, T, Hq, Hk, scale, q_base,
+                                      (T - q_base + fa256::ROWS - 1) / fa256::ROWS * (Hq / 2), one, st);
     flash_kernel<D, GATED, GQA4><<<blocks, FA_THREADS, FaCfg<D>::BYTES, st>>>(
         static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), ldv,
         static_cast<const bf16*>(gate), static_cast<bf16*>(out), lse, T, Hq, Hk, scale * LOG2E, q_base, one);
@@ -923,8 +1235,9 @@ int launch_flash_varlen(const void* q, const void* k, const void* v, int ldv, co
         FaCfg<D>::BYTES);
     if (configured != hipSuccess) return configured;
     constexpr float LOG2E = 1.4426950408889634f;
-    const int nrows = (D == 128 && GQA4) ? fa32::ROWS : GQA4 ? 16 : (D == 256 ? 64 : 128);
-    const int units = GQA4 ? Hq / 4 : Hq;
+    const bool pairs256 = D == 256 && (Hq / Hk) % 2 == 0;
+    const int nrows = (D == 128 && GQA4) ? fa32::ROWS : pairs256 ? fa256::ROWS : GQA4 ? 16 : (D == 256 ? 64 : 128);
+    const int units = pairs256 ? Hq / 2 : GQA4 ? Hq / 4 : Hq;
     for (int s0 = 0; s0 < nseq; s0 += SEQS_MAX) {
         Seqs sq;
         sq.n = min(SEQS_MAX, nseq - s0);
@@ -944,6 +1257,11 @@ int launch_flash_varlen(const void* q, const void* k, const void* v, int ldv, co
         if (blocks == 0) continue;
         if (D == 128 && GQA4) {
             const int e = launch_flash32<GATED>(q, k, v, ldv, gate, out, lse, 0, Hq, Hk, scale, 0, blocks, sq, st);
+            if (e != hipSuccess) return e;
+            continue;
+        }
+        if (pairs256) {
+            const int e = launch_flash256<GATED>(q, k, v, ldv, gate, out, lse, 0, Hq, Hk, scale, 0, blocks, sq, st);
             if (e != hipSuccess) return e;
             continue;
         }
