@@ -135,8 +135,7 @@ def timed(stream, ev, steps, warmup, launches):
     return wall_ms, per
 
 
-def bench_attention(api, st, ev, steps, warmup, T=2048):
-    Hq, Hk, Dh = 16, 4, 128
+def bench_attention(api, st, ev, steps, warmup, T=2048, Hq=16, Hk=4, Dh=128, label="cfg1"):
     rng = np.random.default_rng(1)
     q, k, v, gate = (hip.to_device(bf16(rng, T * h * Dh), st) for h in (Hq, Hk, Hk, Hq))
     out, lse = hip.DeviceBuffer(T * Hq * Dh * 2), hip.DeviceBuffer(Hq * T * 4)
@@ -150,9 +149,10 @@ def bench_attention(api, st, ev, steps, warmup, T=2048):
     kern = per["flash_attention"]
     achieved = flops / (kern * 1e-3) / 1e12
     return {
-        "workload": f"cfg1 gated GQA flash-attention prefill T={T} Hq=16 Hk=4 Dh=128 + fp32 LSE",
+        "workload": f"{label} gated GQA flash-attention prefill T={T} Hq={Hq} Hk={Hk} Dh={Dh} + fp32 LSE",
         "tokens_per_s": T / (wall * 1e-3), "ms_per_step": wall, "kernel_ms": per,
-        "roofline": {"kernel": "flash32_kernel<gated>", "bound": "mfma", "achieved": achieved,
+        "roofline": {"kernel": "flash32_kernel<gated>" if Dh == 128 else "flash256_kernel<gated>", "bound": "mfma",
+                     "achieved": achieved,
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
                      "algorithmic_flop": flops},
     }
@@ -344,7 +344,7 @@ def bench_hbm_ops(api, st, ev, steps, warmup):
     return res
 
 
-def bench_decision_prefill(steps, warmup, T=4096):
+def bench_decision_prefill(steps, warmup, T=4096, tune=False, graph=True):
     """Config 3: one 4096-token decision prefill of the random-init 4B-class hybrid
     decoder (32 layers, 3:1 GDN:attention, hidden 2560, SwiGLU 9728, 16/4 x 256 attention,
     GDN 16 qk / 32 v heads) through the native runner, then the 8-label head on the last
@@ -356,7 +356,8 @@ def bench_decision_prefill(steps, warmup, T=4096):
     cfg = QM.CFG3_4B
     m = QM.Model(cfg, seed=0, max_tokens=T)
     try:
-        m.set_graph(True)
+        m.set_graph(graph)
+        m.set_gemm_tuning(tune)
         rng = np.random.default_rng(4)
         ids = rng.integers(0, cfg.vocab, T).astype(np.int32)
         labels = (np.arange(8) * 997 + 151).astype(np.int32)
@@ -383,13 +384,13 @@ def bench_decision_prefill(steps, warmup, T=4096):
             n_gdn * 180224.0 * T * cfg.lin_v_heads)
     return ms, {"workload": "cfg3 random-init 4B-class hybrid decoder (32 layers, 24 GDN + 8 gated attention), "
                             "T=4096 decision prefill + 8-label head, hipGraph replay",
-                "gemm_plans": gemm_plan_mode(),
+                "gemm_plans": gemm_plan_mode(tune),
                 "ms_per_decision": ms, "argmax": int(np.argmax(logits)),
                 "algorithmic_flop": flop, "achieved_TFLOPs": flop / (ms * 1e-3) / 1e12,
                 "frac_of_bf16_peak": flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
 
-def bench_candidates(steps, warmup, P=2048, n=8):
+def bench_candidates(steps, warmup, P=2048, n=8, tune=False):
     """Config 4: the random-init 27B-class hybrid decoder (64 layers, 3:1, hidden
     5120, 24/4 x 256 attention, GDN 16 qk / 48 v heads, SwiGLU 17408, vocabulary 248320, untied
     LM head). A step captures a 2048-token prefix, then scores 8 candidate continuations of
@@ -405,6 +406,7 @@ def bench_candidates(steps, warmup, P=2048, n=8):
     cands = [rng.integers(0, cfg.vocab, int(k)).astype(np.int32) for k in lens]
     m = QM.Model(cfg, seed=0, max_tokens=P + 256 if sum(lens) <= P + 256 else int(sum(lens)))
     try:
+        m.set_gemm_tuning(tune)
         tw = time.perf_counter()
         for _ in range(max(warmup, 1)):
             m.capture(prefix)
@@ -426,15 +428,15 @@ def bench_candidates(steps, warmup, P=2048, n=8):
     return {"workload": "cfg4 random-init 27B-class hybrid decoder (64 layers), 2048-token prefix captured, "
                         f"{n} candidates of {', '.join(str(int(k)) for k in lens)} tokens scored from it",
             "ms_per_job": (cap + sco) * 1e3 / steps, "capture_ms": cap * 1e3 / steps, "score_ms": sco * 1e3 / steps,
-            "candidate_tokens": int(sum(lens)), "best_candidate": int(np.argmax(scores)), "gemm_plans": gemm_plan_mode(),
+            "candidate_tokens": int(sum(lens)), "best_candidate": int(np.argmax(scores)), "gemm_plans": gemm_plan_mode(tune),
             "scores": [round(float(x), 3) for x in scores]}
 
 
-def gemm_plan_mode():
-    """How cs1_gemm picks its hipBLASLt kernels in this process (CS1_GEMM_TUNE)."""
-    if os.environ.get("CS1_GEMM_TUNE") == "0":
-        return "first heuristic choice per shape (CS1_GEMM_TUNE=0)"
-    return "fastest of the top 16 heuristic candidates per shape, timed on first use"
+def gemm_plan_mode(tune):
+    """How cs1_gemm picks its hipBLASLt kernels in the run."""
+    if tune:
+        return "tuned: fastest of up to 16 heuristic candidates per shape (cs1_gemm_tune on the first eager call)"
+    return "deterministic: hipBLASLt's first heuristic choice per shape (cs1_gemm default)"
 
 
 def cpu_baseline_attention():
@@ -521,6 +523,7 @@ def probe(api, st):
     ev = Events()
     bench_attention(api, st, ev, 3, 0)
     bench_attention(api, st, ev, 3, 0, T=8192)
+    bench_attention(api, st, ev, 3, 0, T=4096, Dh=256)
     bench_gdn(api, st, ev, 3, 0, 8192, 32, 16, True, 0.01, 2, "cfg2")
     bench_gdn(api, st, ev, 3, 0, 512, 16, 16, False, 0.0, 0, "cfg0")
     bench_hbm_ops(api, st, ev, 3, 0)
@@ -638,6 +641,7 @@ def main():
     ap.add_argument("--probe", action="store_true", help="short kernel sequence for rocprofv3 counter passes")
     ap.add_argument("--no-model", action="store_true", help="skip the config-3 and config-4 model runs")
     ap.add_argument("--models-only", action="store_true", help="only the config-3 and config-4 model runs")
+    ap.add_argument("--no-graph", action="store_true", help="config 3 without hipGraph replay (eager launches)")
     ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR", help="summarize rocprofv3 --pmc output of --probe")
     ap.add_argument("--summarize-trace", nargs="+", metavar="DIR", help="summarize rocprofv3 --kernel-trace output")
     args = ap.parse_args()
@@ -658,13 +662,18 @@ def main():
         probe(api, st)
         return
     if args.models_only:
-        dec_ms, dec = bench_decision_prefill(min(args.steps, 10), args.warmup)
-        print(json.dumps({"decision_prefill_ms_4k": dec_ms, "model_cfg3": dec,
-                          "model_cfg4": bench_candidates(min(args.steps, 3), 1)}), flush=True)
+        dec_ms, dec = bench_decision_prefill(min(args.steps, 10), args.warmup, graph=not args.no_graph)
+        dec["graph"] = not args.no_graph
+        dec["tuned_gemm_ms_per_decision"] = bench_decision_prefill(min(args.steps, 10), args.warmup, tune=True,
+                                                                   graph=not args.no_graph)[0]
+        cand = bench_candidates(min(args.steps, 3), 1)
+        cand["tuned_gemm_ms_per_job"] = bench_candidates(min(args.steps, 3), 1, tune=True)["ms_per_job"]
+        print(json.dumps({"decision_prefill_ms_4k": dec_ms, "model_cfg3": dec, "model_cfg4": cand}), flush=True)
         return
     ev = Events()
     attn = bench_attention(api, st, ev, args.steps, args.warmup)
-    attn8k = bench_attention(api, st, ev, max(2, args.steps // 4), 1, T=8192)
+    attn8k = bench_attention(api, st, ev, max(2, args.steps // 4), 1, T=8192, label="north-star shape")
+    attn256 = bench_attention(api, st, ev, max(2, args.steps // 2), 1, T=4096, Dh=256, label="cfg3 layer")
     g2 = bench_gdn(api, st, ev, args.steps, args.warmup, 8192, 32, 16, True, 0.01, 2,
                    "cfg2 conv1d(k=4)+SiLU then GDN chunked prefill T=8192 HK=16 H=32 D=128, S0~N(0,0.01)")
     g0 = bench_gdn(api, st, ev, args.steps, args.warmup, 512, 16, 16, False, 0.0, 0,
@@ -673,6 +682,9 @@ def main():
     gref = bench_gdn_reference_shapes(api, st, ev)
     dec_ms, dec = (None, None) if args.no_model else bench_decision_prefill(min(args.steps, 10), args.warmup)
     cand = None if args.no_model else bench_candidates(min(args.steps, 3), 1)
+    if not args.no_model:
+        dec["tuned_gemm_ms_per_decision"] = bench_decision_prefill(min(args.steps, 10), args.warmup, tune=True)[0]
+        cand["tuned_gemm_ms_per_job"] = bench_candidates(min(args.steps, 3), 1, tune=True)["ms_per_job"]
     cpu = None if args.no_cpu else cpu_baseline_attention()
     if not args.no_cpu:
         g0["cpu_baseline"] = cpu_baseline_gdn_cfg0()
@@ -686,7 +698,8 @@ def main():
         "roofline": {k: attn["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac")} |
                     {"traffic": traffic_bytes("q35::(anonymous namespace)::flash32_kernel<true, false> grid=131072 ")},
         "cpu_baseline": cpu,
-        "layers": {"attention_cfg1": attn, "attention_t8192": attn8k, "gdn_cfg2": g2, "gdn_cfg0": g0},
+        "layers": {"attention_cfg1": attn, "attention_t8192": attn8k, "attention_cfg3_dh256": attn256,
+                   "gdn_cfg2": g2, "gdn_cfg0": g0},
         "hbm_ops": hbm,
         "calibration": cal,
         "gdn_reference_shapes": gref,

@@ -728,7 +728,7 @@ __global__ void __launch_bounds__(256) state_pass(const float4* __restrict__ s_i
 // result (the reference's two-phase == one-shot invariant). Segments reuse the start of the
 // workspace; two float32 [H, 128, 128] states after the records alternate between them.
 #ifndef Q35_SEG_MB
-#define Q35_SEG_MB 150
+#define Q35_SEG_MB 200
 #endif
 constexpr size_t SEG_BYTES = (size_t)Q35_SEG_MB << 20;
 constexpr size_t REC_BYTES = 72 * 1024;

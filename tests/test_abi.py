@@ -46,7 +46,7 @@ def test_workspace_size_is_pure_and_monotone(api):
     assert a == api.cs1_gdn_workspace_floats(1, 4) > 0
     assert api.cs1_gdn_workspace_floats(65, 4) > a
     # per (head, chunk): w, u, qd, kd^T (64x128 bf16) + pb (64x64 bf16) + decay, 256-B aligned parts;
-    # a sequence long enough to run in segments (records > 150 MiB) adds two float32 states
+    # a sequence long enough to run in segments (records > 200 MiB) adds two float32 states
     rec = 4 * 64 * 128 * 2 + 64 * 64 * 2
     mid = api.cs1_gdn_workspace_floats(4096, 32) * 4
     assert 32 * 64 * rec <= mid < 32 * 64 * (rec + 4) + 4096

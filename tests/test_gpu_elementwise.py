@@ -204,6 +204,27 @@ def test_sigmoid_gate_vector_and_scalar():
     assert ulp_diff(get_bf16(dx2, n, 2), O.sigmoid_gate(x[1:], g[1:])) <= 1
 
 
+@pytest.mark.parametrize("label,n", [("cfg1", 2048 * 16 * 128), ("cfg3", 4096 * 16 * 256)])
+def test_gate_sigmoid_deviation_bounded_at_benchmark_shapes(label, n):
+    """The output gate's sigmoid uses the hardware exp2 and reciprocal instead of the reference's
+    expf form (attention.cu:228), a deliberate deviation: at the gate sizes of configs 1 and 3
+    (gate logits and values N(0, 1), as in the benchmark) every gated value stays within one
+    bf16 step of the expf emulator and at least 99.5% are identical."""
+    api, st = hip.api(), stream()
+    say(f"gate sigmoid deviation at the {label} shape, n={n}")
+    rng = np.random.default_rng(7)
+    x = O.f32_to_bf16(rng.standard_normal(n).astype(np.float32))
+    g = O.f32_to_bf16(rng.standard_normal(n).astype(np.float32))
+    dx, dg = dev(x), dev(g)
+    hip.check(api.cs1_sigmoid_gate(dx.at(0), dg.at(0), n, st.handle), "gate")
+    got = get_bf16(dx, n)
+    want = O.sigmoid_gate(x, g)
+    same = float(np.mean(got == want))
+    say(f"  identical to the expf form: {same:.5f}, max ulp {ulp_diff(got, want)}")
+    assert ulp_diff(got, want) <= 1
+    assert same >= 0.995
+
+
 def test_embed_and_device_copies():
     api, st = hip.api(), stream()
     V, D, T = 1000, 2560, 257

@@ -114,7 +114,7 @@ def test_config2_gdn_at_full_size():
 
 
 def test_gdn_prefill_two_phase_matches_one_shot_bit_for_bit():
-    """kernels.rs:1049-1054; the 8192- and 8229-token cases run in segments (records over 150
+    """kernels.rs:1049-1054; the 8192- and 8229-token cases run in segments (records over 200
     MiB), so they also check that segmentation is invisible in the result."""
     api, st = hip.api(), stream()
     for t, h, hk, amp, decay in [(107, 4, 2, 1.0, 1.0), (936, 4, 2, 0.01, 1.0), (3399, 3, 1, 0.01, 1.0),
