@@ -168,7 +168,8 @@ constexpr int PLANE = 4 * 4 * 1024;                // [4 blocks][4 steps] fragme
 constexpr int R0_TM = 0;
 constexpr int R0_TB = R0_TM + C * FLD * 4;         // 16640
 constexpr int R0_SC = R0_TB + C * TLD * 2;         // 25856
-constexpr int R1 = R0 + 2 * PLANE;                 // A float [64][65]
+constexpr int R1 = R0 + 2 * PLANE;                 // A float [64][65]; then raw k fragments
+static_assert(C * FLD * 4 >= 16 * (int)FRAG * 16, "region 1 holds the 16 raw k fragments");
 constexpr int R2 = R1 + C * FLD * 4;               // cum, beta, e^cum, e^(last-cum), k inverse norm
 constexpr int PREP_SMEM = R2 + 5 * C * 4;
 static_assert(R0_SC + 4 * 256 * 4 <= R1, "region 0 overlay fits");
@@ -241,11 +242,13 @@ __global__ void __launch_bounds__(PT)
     const int t0 = cl * C;
     Q35_PHASE_START();
 
-    // 0. loads: own k rows (block `wave`), q rows (block 3 - wave), and the k and v columns
-    //    of dim step `wave` for all 64 tokens; gates for all tokens (lane = token)
+    // 0. loads: own k rows (block `wave`), q rows (block 3 - wave), and the v columns of dim
+    //    step `wave` for all 64 tokens; gates for all tokens (lane = token). The k columns
+    //    step 6 needs are the other waves' raw k rows, passed through LDS there rather than
+    //    loaded a second time.
     const int qb = 3 - wave;
     const int krow = 16 * wave + col, qrow = 16 * qb + col;
-    u32x4 kraw[4], qraw[4], kc[4], vc[4];
+    u32x4 kraw[4], qraw[4], vc[4];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
         kraw[s] = load_perm(k + ((size_t)(t0 + krow) * HK + hk) * DK, s, grp, t0 + krow < T);
@@ -254,7 +257,6 @@ __global__ void __launch_bounds__(PT)
 #pragma unroll
     for (int tb_ = 0; tb_ < 4; tb_++) {
         const int t = t0 + 16 * tb_ + col;
-        kc[tb_] = load_perm(k + ((size_t)t * HK + hk) * DK, wave, grp, t < T);
         vc[tb_] = load_perm(v + ((size_t)t * H + h) * DK, wave, grp, t < T);
     }
     const int tl = t0 + lane;
@@ -427,7 +429,9 @@ __global__ void __launch_bounds__(PT)
     }
     Q35_PHASE(5);
 
-    // 5. Tb = bf16(T beta_j)
+    // 5. Tb = bf16(T beta_j); the raw k rows go to region 1 (A is dead) for step 6
+#pragma unroll
+    for (int s = 0; s < 4; s++) reinterpret_cast<u32x4*>(am)[(wave * 4 + s) * FRAG + lane] = kraw[s];
     for (int x = tid; x < C * C; x += PT) {
         const int i = x / C, j = x % C;
         tb[i * TLD + j] = to_bf16(tm[i * FLD + j] * bet[j]);
@@ -448,7 +452,7 @@ __global__ void __launch_bounds__(PT)
             const int tb_ = 2 * s + p, row = 16 * tb_ + col;
             const float ki = kinv_s[row], e1 = ecum[row], e2 = erem[row];
             float kf[8], a1[8], a2[8];
-            unpack8v(kc[tb_], kf);
+            unpack8v(reinterpret_cast<const u32x4*>(am)[(tb_ * 4 + wave) * FRAG + lane], kf);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const float kx = kf[e] * ki;
