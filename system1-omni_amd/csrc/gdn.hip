@@ -30,13 +30,15 @@
 //         float32 MFMA v_mfma_f32_16x16x4_f32;
 //       - every scan operand is written to the workspace in the exact per-lane order the
 //         scan's MFMA consumes it (1 KB per wave per store, fully coalesced).
-//   * gdn_scan, grid (head x 8 slices of 16 value columns), 4 waves.  The float32 state
-//     slice 128 x 16 lives in MFMA accumulators; each chunk streams its operand
+//   * gdn_scan, grid (head x 8 slices of 16 value columns, or x 4 slices of 32 when that
+//     needs fewer rounds of blocks), 4 chain waves + 4 output waves.  The float32 state
+//     slice 128 x 16 (per half) lives in MFMA accumulators; each chunk streams its operand
 //     fragments from HBM/L2 straight into registers (three chunks ahead) and exchanges only
 //     bf16(S) and v_new through LDS.  The output o = qd Sb + pb v_new is produced in the
 //     same pass, so per-chunk states and v_new never go to memory.  The slices of one head
 //     run on the same XCD (block = slice * H + head) and share its L2.
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 
 #include "common.h"
@@ -502,15 +504,15 @@ __global__ void __launch_bounds__(PT)
 // ------------------------------------------------------------------ gdn_scan
 
 constexpr int ST = 512;   // threads: waves 0-3 carry the state, waves 4-7 the output
-constexpr int BV = 16;    // value columns per block
-constexpr int NS = DK / BV;
-constexpr int SLD = DK + 8;  // bf16 stride of Sb^T [16][128]
-constexpr int VLD = C + 8;   // bf16 stride of v_new^T [16][64]
+constexpr int BV = 16;    // value columns per MFMA tile; a block owns NSUB such halves
+constexpr int SLD = DK + 8;  // bf16 stride of Sb^T [16 NSUB][128]
+constexpr int VLD = C + 8;   // bf16 stride of v_new^T [16 NSUB][64]
 
+template <int NSUB>
 struct ChainOps {
-    u32x4 w[4];     // w fragments (row block = wave, dim steps)
-    u32x4 kd[2][2]; // kd^T fragments (dim blocks 2 wave + i, token steps)
-    u32x2 u;        // u tile (row block = wave, dim block = slice)
+    u32x4 w[4];        // w fragments (row block = wave, dim steps)
+    u32x4 kd[2][2];    // kd^T fragments (dim blocks 2 wave + i, token steps)
+    u32x2 u[NSUB];     // u tiles (row block = wave, dim blocks NSUB slice + half)
     float decay;
 };
 
@@ -535,7 +537,8 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-__device__ __forceinline__ void load_chain(ChainOps& op, const Streams& sr, const float* decay, int c, int rb,
+template <int NSUB>
+__device__ __forceinline__ void load_chain(ChainOps<NSUB>& op, const Streams& sr, const float* decay, int c, int rb,
                                            int lane, int slice) {
     const int v16 = lane * 16;
     const int rec_w = c * 16 * 1024 + rb * 4 * 1024;
@@ -543,9 +546,10 @@ __device__ __forceinline__ void load_chain(ChainOps& op, const Streams& sr, cons
     for (int s = 0; s < 4; s++) op.w[s] = bload16(sr.w, v16 + s * 1024, rec_w);
 #pragma unroll
     for (int i = 0; i < 4; i++) op.kd[i >> 1][i & 1] = bload16(sr.kd, v16 + i * 1024, rec_w);
-    const u32x2 uu = __builtin_bit_cast(
-        u32x2, __builtin_amdgcn_raw_buffer_load_b64(sr.u, lane * 8, c * 32 * 512 + (rb * 8 + slice) * 512, 0));
-    op.u = uu;
+#pragma unroll
+    for (int hf = 0; hf < NSUB; hf++)
+        op.u[hf] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                 sr.u, lane * 8, c * 32 * 512 + (rb * 8 + NSUB * slice + hf) * 512, 0));
     op.decay = decay[c];
 }
 
@@ -569,18 +573,26 @@ __device__ __forceinline__ u32x4 lds_perm(const bf16* base, int ld, int col, int
 // output: acc = qd Sb]  B  [chain: S = S decay + kd^T v_new; output: o = acc + pb v_new].
 // Chain waves read Sb only between A and B; output waves read v_new after B and are done
 // before the next A, when v_new is rewritten.
+//
+// A block owns NSUB 16-column halves of one head's value columns (NSUB = 1: 16 columns, eight
+// slice blocks per head; NSUB = 2: 32 columns, four). Every half runs the same instructions
+// on the same operand fragments as a one-half block would, so both forms give the same bits;
+// the two-half form fetches each chunk's shared w / kd / qd / pb fragments once for two halves
+// and is used when it needs fewer rounds of blocks on the device (gdn_launch).
+template <int NSUB>
 __global__ void __launch_bounds__(ST)
     gdn_scan(Work ws, const float* __restrict__ decay_all, bf16* __restrict__ o, int T, int H, int NC,
              const float* __restrict__ s_in, size_t s_in_stride, float* __restrict__ s_out, size_t s_out_stride,
              const GSeqs gs) {
-    __shared__ __align__(16) bf16 sbt[BV * SLD];
-    __shared__ __align__(16) bf16 vnt[BV * VLD];
-    const int h = blockIdx.x % H, slice = (blockIdx.x / H) % NS, v0 = slice * BV;
+    constexpr int BVB = BV * NSUB, NSB = DK / BVB;
+    __shared__ __align__(16) bf16 sbt[BVB * SLD];
+    __shared__ __align__(16) bf16 vnt[BVB * VLD];
+    const int h = blockIdx.x % H, slice = (blockIdx.x / H) % NSB, v0 = slice * BVB;
     size_t rec0 = (size_t)h * NC;
     if (gs.n > 0) {
         // packed sequences: blocks (sequence, slice, head); each sequence is scanned alone
         // from its own (or the shared) initial state over its own chunks
-        const int sq = blockIdx.x / (H * NS);
+        const int sq = blockIdx.x / (H * NSB);
         rec0 += gs.chk[sq];
         NC = gs.chk[sq + 1] - gs.chk[sq];
         T = gs.tok[sq + 1] - gs.tok[sq];
@@ -591,8 +603,8 @@ __global__ void __launch_bounds__(ST)
             // an empty sequence: its final state is its initial state (the whole block leaves
             // here, before any barrier)
             if (s_out != nullptr && tid_of_block() < 128)
-                for (int x = tid_of_block(); x < DK * BV; x += 128) {
-                    const size_t at_ = ((size_t)h * DK + x / BV) * DK + v0 + x % BV;
+                for (int x = tid_of_block(); x < DK * BVB; x += 128) {
+                    const size_t at_ = ((size_t)h * DK + x / BVB) * DK + v0 + x % BVB;
                     s_out[at_] = s_in ? s_in[at_] : 0.f;
                 }
             return;
@@ -609,47 +621,65 @@ __global__ void __launch_bounds__(ST)
     const float* decay = decay_all + rec0;  // read-only kernel argument: scalar loads
 
     if (chain) {
-        // state rows 32 rb + 16 i + 4 grp + r, column v0 + col
-        f32x4 st[2];
+        // state rows 32 rb + 16 i + 4 grp + r, column v0 + 16 hf + col
+        f32x4 st[NSUB][2];
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                st[i][r] = s_in ? s_in[((size_t)h * DK + 32 * rb + 16 * i + 4 * grp + r) * DK + v0 + col] : 0.f;
-        Q35_LPHASE_START();
-        auto step = [&](const ChainOps& cur) {
+        for (int hf = 0; hf < NSUB; hf++)
 #pragma unroll
             for (int i = 0; i < 2; i++)
-                *reinterpret_cast<u32x2*>(sbt + col * SLD + 32 * rb + 16 * i + 4 * grp) =
-                    u32x2{pack2(st[i][0], st[i][1]), pack2(st[i][2], st[i][3])};
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    st[hf][i][r] = s_in ? s_in[((size_t)h * DK + 32 * rb + 16 * i + 4 * grp + r) * DK + v0 + 16 * hf + col]
+                                        : 0.f;
+        Q35_LPHASE_START();
+        auto step = [&](const ChainOps<NSUB>& cur) {
+#pragma unroll
+            for (int hf = 0; hf < NSUB; hf++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    *reinterpret_cast<u32x2*>(sbt + (16 * hf + col) * SLD + 32 * rb + 16 * i + 4 * grp) =
+                        u32x2{pack2(st[hf][i][0], st[hf][i][1]), pack2(st[hf][i][2], st[hf][i][3])};
             Q35_LPHASE(8);
             __syncthreads();  // A
             Q35_LPHASE(9);
-            u32x4 sb[4];
+            u32x4 sb[NSUB][4];
 #pragma unroll
-            for (int s = 0; s < 4; s++) sb[s] = lds_perm(sbt, SLD, col, s, grp);
-            __builtin_amdgcn_sched_barrier(0);  // all four reads in flight before the first MFMA
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            for (int hf = 0; hf < NSUB; hf++)
 #pragma unroll
-            for (int s = 0; s < 4; s++) acc = mfma16(cur.w[s], sb[s], acc);
-            const float vn0 = lo_f32(cur.u[0]) - acc[0], vn1 = hi_f32(cur.u[0]) - acc[1];
-            const float vn2 = lo_f32(cur.u[1]) - acc[2], vn3 = hi_f32(cur.u[1]) - acc[3];
-            *reinterpret_cast<u32x2*>(vnt + col * VLD + 16 * rb + 4 * grp) = u32x2{pack2(vn0, vn1), pack2(vn2, vn3)};
+                for (int s = 0; s < 4; s++) sb[hf][s] = lds_perm(sbt + 16 * hf * SLD, SLD, col, s, grp);
+            __builtin_amdgcn_sched_barrier(0);  // all the reads in flight before the first MFMA
+#pragma unroll
+            for (int hf = 0; hf < NSUB; hf++) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 4; s++) acc = mfma16(cur.w[s], sb[hf][s], acc);
+                const float vn0 = lo_f32(cur.u[hf][0]) - acc[0], vn1 = hi_f32(cur.u[hf][0]) - acc[1];
+                const float vn2 = lo_f32(cur.u[hf][1]) - acc[2], vn3 = hi_f32(cur.u[hf][1]) - acc[3];
+                *reinterpret_cast<u32x2*>(vnt + (16 * hf + col) * VLD + 16 * rb + 4 * grp) =
+                    u32x2{pack2(vn0, vn1), pack2(vn2, vn3)};
+            }
             Q35_LPHASE(10);
             __syncthreads();  // B
             Q35_LPHASE(11);
-            const u32x4 vb0 = lds_perm(vnt, VLD, col, 0, grp), vb1 = lds_perm(vnt, VLD, col, 1, grp);
+            u32x4 vb[NSUB][2];
+#pragma unroll
+            for (int hf = 0; hf < NSUB; hf++) {
+                vb[hf][0] = lds_perm(vnt + 16 * hf * VLD, VLD, col, 0, grp);
+                vb[hf][1] = lds_perm(vnt + 16 * hf * VLD, VLD, col, 1, grp);
+            }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                st[i] *= cur.decay;
-                st[i] = mfma16(cur.kd[i][0], vb0, st[i]);
-                st[i] = mfma16(cur.kd[i][1], vb1, st[i]);
-            }
+            for (int hf = 0; hf < NSUB; hf++)
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    st[hf][i] *= cur.decay;
+                    st[hf][i] = mfma16(cur.kd[i][0], vb[hf][0], st[hf][i]);
+                    st[hf][i] = mfma16(cur.kd[i][1], vb[hf][1], st[hf][i]);
+                }
             Q35_LPHASE(12);
         };
         // four rotating operand sets: chunk c + 3 is requested while chunk c is processed
-        ChainOps opa, opb, opc, opd;
+        ChainOps<NSUB> opa, opb, opc, opd;
         load_chain(opa, sr, decay, at(0), rb, lane, slice);
         load_chain(opb, sr, decay, at(1), rb, lane, slice);
         load_chain(opc, sr, decay, at(2), rb, lane, slice);
@@ -669,30 +699,46 @@ __global__ void __launch_bounds__(ST)
         Q35_LPHASE_FLUSH();
         if (s_out) {
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int hf = 0; hf < NSUB; hf++)
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    s_out[((size_t)h * DK + 32 * rb + 16 * i + 4 * grp + r) * DK + v0 + col] = st[i][r];
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        s_out[((size_t)h * DK + 32 * rb + 16 * i + 4 * grp + r) * DK + v0 + 16 * hf + col] = st[hf][i][r];
         }
     } else {
         auto step = [&](const OutOps& cur, int c) {
             __syncthreads();  // A
-            u32x4 sb[4];
+            u32x4 sb[NSUB][4];
 #pragma unroll
-            for (int s = 0; s < 4; s++) sb[s] = lds_perm(sbt, SLD, col, s, grp);
+            for (int hf = 0; hf < NSUB; hf++)
+#pragma unroll
+                for (int s = 0; s < 4; s++) sb[hf][s] = lds_perm(sbt + 16 * hf * SLD, SLD, col, s, grp);
             __builtin_amdgcn_sched_barrier(0);
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            f32x4 acc[NSUB];
 #pragma unroll
-            for (int s = 0; s < 4; s++) acc = mfma16(cur.qd[s], sb[s], acc);
+            for (int hf = 0; hf < NSUB; hf++) {
+                acc[hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 4; s++) acc[hf] = mfma16(cur.qd[s], sb[hf][s], acc[hf]);
+            }
             __syncthreads();  // B
-            const u32x4 vb0 = lds_perm(vnt, VLD, col, 0, grp), vb1 = lds_perm(vnt, VLD, col, 1, grp);
-            __builtin_amdgcn_sched_barrier(0);
-            acc = mfma16(cur.pb[0], vb0, acc);
-            acc = mfma16(cur.pb[1], vb1, acc);
+            u32x4 vb[NSUB][2];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int t = c * C + 16 * rb + 4 * grp + r;
-                if (t < T) o[((size_t)t * H + h) * DK + v0 + col] = to_bf16(acc[r]);
+            for (int hf = 0; hf < NSUB; hf++) {
+                vb[hf][0] = lds_perm(vnt + 16 * hf * VLD, VLD, col, 0, grp);
+                vb[hf][1] = lds_perm(vnt + 16 * hf * VLD, VLD, col, 1, grp);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int hf = 0; hf < NSUB; hf++) {
+                acc[hf] = mfma16(cur.pb[0], vb[hf][0], acc[hf]);
+                acc[hf] = mfma16(cur.pb[1], vb[hf][1], acc[hf]);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int t = c * C + 16 * rb + 4 * grp + r;
+                    if (t < T) o[((size_t)t * H + h) * DK + v0 + 16 * hf + col] = to_bf16(acc[hf][r]);
+                }
             }
         };
         OutOps opa, opb, opc, opd;
@@ -758,6 +804,30 @@ Plan plan_segments(int T, int H) {
     return p;
 }
 
+// Halves per scan block: one 8-wave scan block fits a CU, so `units` (heads x sequences)
+// blocks of NSUB halves run in ceil(units * 8 / NSUB / CUs) rounds. The two-half block's chunk
+// step is ~1.46x the one-half block's (measured alone on the device: 1.24 vs 0.85 us), so it
+// is chosen when it saves enough rounds (config 2's 32 heads: one round either way, one half;
+// 48 heads: two rounds against one, two halves). Overridable for tests by Q35_SCAN_HALVES.
+int scan_halves(int units) {
+    if (const char* e = getenv("Q35_SCAN_HALVES")) {
+        const int v = atoi(e);
+        if (v == 1 || v == 2) return v;
+    }
+    constexpr int MAX_DEV = 64;
+    static int cus_of[MAX_DEV];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 1;
+    if (cus_of[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 1;
+        cus_of[dev] = n;
+    }
+    const long cus = cus_of[dev];
+    const long r1 = ((long)units * 8 + cus - 1) / cus, r2 = ((long)units * 4 + cus - 1) / cus;
+    return 146 * r2 < 100 * r1 ? 2 : 1;
+}
+
 // One launch pair over packed sequences (gs.n > 0: T is the total row count and gs
 // describes the sequences, their chunk offsets filled here) or over one sequence (or one
 // segment of it) of T rows.
@@ -779,9 +849,11 @@ int gdn_launch(const void* q, const void* k, const void* v, const float* g, cons
     gdn_prep<<<dim3(NC, H), PT, PREP_SMEM, st>>>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
                                                  static_cast<const bf16*>(v), g, static_cast<const bf16*>(beta), ws, T,
                                                  H, HK, scale, gs);
-    gdn_scan<<<H * NS * nseq, ST, 0, st>>>(ws, ws.decay, static_cast<bf16*>(o), T, H, NC,
-                                          static_cast<const float*>(s_in), s_in_stride, static_cast<float*>(s_out),
-                                          s_out_stride, gs);
+    const int halves = scan_halves(H * nseq);
+    auto scan = halves == 2 ? gdn_scan<2> : gdn_scan<1>;
+    scan<<<H * (DK / (BV * halves)) * nseq, ST, 0, st>>>(ws, ws.decay, static_cast<bf16*>(o), T, H, NC,
+                                                        static_cast<const float*>(s_in), s_in_stride,
+                                                        static_cast<float*>(s_out), s_out_stride, gs);
     return hipGetLastError();
 }
 

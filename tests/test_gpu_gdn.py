@@ -138,6 +138,43 @@ def test_gdn_prefill_two_phase_matches_one_shot_bit_for_bit():
         np.testing.assert_array_equal(get(so, np.float32, h * D * D).reshape(h, D, D), s1)
 
 
+@pytest.mark.parametrize("t,h,hk,varlen", [(1000, 48, 16, False), (3399, 48, 16, False), (300, 32, 16, False),
+                                            (0, 48, 16, True)])
+def test_gdn_scan_block_forms_are_bit_identical(t, h, hk, varlen, monkeypatch):
+    """The scan runs one or two 16-column halves per block (chosen by how many rounds of
+    blocks the device needs: two halves at 48 heads, one at 32). Both forms must give the same
+    bits, for single sequences with an initial state and for packed sequences."""
+    api, st = hip.api(), stream()
+    say(f"gdn scan block forms t={t} h={h} hk={hk} varlen={varlen}")
+    if not varlen:
+        q, k, v, g, b, s0 = cfg0_inputs(t, h, hk, seed=5, s0_std=0.01)
+        runs = []
+        for halves in ("1", "2"):
+            monkeypatch.setenv("Q35_SCAN_HALVES", halves)
+            runs.append(run_gdn(q, k, v, g, b, t, h, hk, s_in=s0, want_state=True))
+        np.testing.assert_array_equal(runs[0][0], runs[1][0])
+        np.testing.assert_array_equal(runs[0][1], runs[1][1])
+        return
+    lens = [64, 1, 0, 200, 129]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    q, k, v, g, b, _ = cfg0_inputs(T, h, hk, seed=6)
+    s0 = (np.random.default_rng(7).standard_normal((h, D, D)) * 0.01).astype(np.float32)
+    dq, dk, dv, dg, db, si = dev(q), dev(k), dev(v), dev(g), dev(b), dev(s0)
+    outs = []
+    for halves in ("1", "2"):
+        monkeypatch.setenv("Q35_SCAN_HALVES", halves)
+        o = empty(T * h * D * 2)
+        so = empty(len(lens) * h * D * D * 4)
+        ws = empty(api.cs1_gdn_workspace_floats(T + 64 * len(lens), h) * 4)
+        hip.check(api.cs1_gdn_prefill_varlen(dq.at(0), dk.at(0), dv.at(0), dg.at(0), db.at(0), o.at(0), ws.at(0),
+                                             cu.ctypes.data, len(lens), h, hk, D ** -0.5, si.at(0), 0, so.at(0),
+                                             h * D * D, st.handle), "varlen")
+        outs.append((get_bf16(o, T * h * D), get(so, np.float32, len(lens) * h * D * D)))
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+
+
 def test_gdn_empty_window_captures_state_copy_and_zero_initial_state():
     # kernels.rs:692-742: T = 0 under graph capture must re-run the copy / zero on replay
     api, st = hip.api(), stream()
