@@ -38,6 +38,7 @@
 //     same pass, so per-chunk states and v_new never go to memory.  The slices of one head
 //     run on the same XCD (block = slice * H + head) and share its L2.
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <mutex>
 
@@ -815,15 +816,15 @@ int scan_halves(int units) {
         if (v == 1 || v == 2) return v;
     }
     constexpr int MAX_DEV = 64;
-    static int cus_of[MAX_DEV];
+    static std::atomic<int> cus_of[MAX_DEV];  // 0: not looked up yet
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 1;
-    if (cus_of[dev] == 0) {
-        int n = 0;
+    int n = cus_of[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 1;
-        cus_of[dev] = n;
+        cus_of[dev].store(n, std::memory_order_relaxed);
     }
-    const long cus = cus_of[dev];
+    const long cus = n;
     const long r1 = ((long)units * 8 + cus - 1) / cus, r2 = ((long)units * 4 + cus - 1) / cus;
     return 146 * r2 < 100 * r1 ? 2 : 1;
 }
