@@ -19,7 +19,8 @@
 //     k = {4g .. 4g+3, 16+4g .. 16+4g+3}.  With that ordering the accumulators of two
 //     16-row tiles (rows 4g + r of each) are, lane for lane, the B (or A) operand of the
 //     next MFMA, so products chain without moving data between lanes.
-//   * gdn_prep, grid (chunk, head), 4 waves, ~50 KB LDS (three blocks per CU):
+//   * gdn_prep, grid (chunk, head), 4 waves, ~50 KB LDS (three blocks per CU); gdn_prep8, the
+//     same arithmetic on 8 waves, when every item of the launch has a CU of its own:
 //       - TF32 pair products on the bf16 MFMA: each TF32 operand is split exactly into
 //         hi = rne_bf16(x) and lo = x - hi (TF32 has 11 significant bits), and the four
 //         products hi.hi + hi.lo + lo.hi + lo.lo reproduce the TF32 product exactly;
@@ -502,6 +503,355 @@ __global__ void __launch_bounds__(PT)
     Q35_PHASE(7);
 }
 
+// gdn_prep8: the same per-item arithmetic as gdn_prep on eight waves, for launches whose items
+// all fit on the device at once (one block per CU), where a block's latency sets the time:
+//   * waves 0-3 load and normalise k row block `wave`, waves 4-7 q row block `wave - 4` (and the
+//     v columns of dim step `wave - 4`); both sides write their TF32 planes to LDS;
+//   * the ten A tiles and the six pb fragments (ten P tiles) go to the eight waves by a fixed
+//     table, two or three tiles each, both operands from the LDS planes;
+//   * the inverse runs on waves 0-3 as in gdn_prep;
+//   * step 6 splits by product: waves 4-7 transpose v and kd and form u = Tb v (and the kd
+//     fragments), waves 0-3 transpose kw and form w^T, each for dim step `wave & 3`.
+// Every tile, fragment and store is computed by the same instruction sequence on the same
+// values as in gdn_prep, so the records are bit for bit the same.
+constexpr int PT8 = 512;
+constexpr int QPL = PREP_SMEM;                         // q^ planes: hi then lo, [4 blocks][4 steps]
+constexpr int PREP8_SMEM = QPL + 2 * PLANE;
+
+// A tile (i, j) of the chunk: A_ij for the rows of k block i and the columns of k block j
+__device__ __forceinline__ void prep8_a_tile(int bi, int bj, const u32x4* khi_pl, const u32x4* klo_pl, float* am,
+                                             const float* cum, const float* bet, int lane) {
+    const int col = lane & 15, grp = lane >> 4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const u32x4 ah = khi_pl[(bi * 4 + s) * FRAG + lane], al = klo_pl[(bi * 4 + s) * FRAG + lane];
+        const u32x4 bh = khi_pl[(bj * 4 + s) * FRAG + lane], bl = klo_pl[(bj * 4 + s) * FRAG + lane];
+        acc = mfma16(al, bl, acc);
+        acc = mfma16(al, bh, acc);
+        acc = mfma16(ah, bl, acc);
+        acc = mfma16(ah, bh, acc);
+    }
+    const int j = 16 * bj + col;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int i = 16 * bi + 4 * grp + r;
+        const float dec = j <= i ? expf(cum[i] - cum[j]) : 0.f;
+        am[i * FLD + j] = j < i ? bet[i] * acc[r] * dec : 0.f;
+    }
+}
+
+// pb fragment (qb, s): P^T tiles 2 s and 2 s + 1 of q block qb (zero past the diagonal)
+__device__ __forceinline__ void prep8_p_frag(int qb, int s2, const u32x4* khi_pl, const u32x4* klo_pl,
+                                             const u32x4* qhi_pl, const u32x4* qlo_pl, const float* cum,
+                                             const Work& ws, size_t rec, int lane) {
+    const int col = lane & 15, grp = lane >> 4;
+    f32x4 pt[2];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int jt = 2 * s2 + p;
+        pt[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (jt > qb) continue;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const u32x4 ah = khi_pl[(jt * 4 + s) * FRAG + lane], al = klo_pl[(jt * 4 + s) * FRAG + lane];
+            const u32x4 qh = qhi_pl[(qb * 4 + s) * FRAG + lane], ql = qlo_pl[(qb * 4 + s) * FRAG + lane];
+            pt[p] = mfma16(al, ql, pt[p]);
+            pt[p] = mfma16(al, qh, pt[p]);
+            pt[p] = mfma16(ah, ql, pt[p]);
+            pt[p] = mfma16(ah, qh, pt[p]);
+        }
+        const int i = 16 * qb + col;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int j = 16 * jt + 4 * grp + r;
+            pt[p][r] = j <= i ? round_bf16(pt[p][r] * expf(cum[i] - cum[j])) : 0.f;
+        }
+    }
+    ws.pb[(rec * 8 + qb * 2 + s2) * FRAG + lane] = pack_pair(pt[0], pt[1]);
+}
+
+__global__ void __launch_bounds__(PT8)
+    gdn_prep8(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+              const float* __restrict__ g, const bf16* __restrict__ beta, Work ws, int T, int H, int HK, float scale,
+              const GSeqs gs) {
+    extern __shared__ __align__(16) unsigned char sm[];
+    u32x4* khi_pl = reinterpret_cast<u32x4*>(sm + R0);
+    u32x4* klo_pl = reinterpret_cast<u32x4*>(sm + R0 + PLANE);
+    u32x4* qhi_pl = reinterpret_cast<u32x4*>(sm + QPL);
+    u32x4* qlo_pl = reinterpret_cast<u32x4*>(sm + QPL + PLANE);
+    float* tm = reinterpret_cast<float*>(sm + R0_TM);
+    bf16* tb = reinterpret_cast<bf16*>(sm + R0_TB);
+    float* am = reinterpret_cast<float*>(sm + R1);
+    float* cum = reinterpret_cast<float*>(sm + R2);
+    float* bet = cum + C;
+    float* ecum = bet + C;
+    float* erem = ecum + C;
+    float* kinv_s = erem + C;
+
+    const int c = blockIdx.x, h = blockIdx.y, NC = gridDim.x;
+    int cl = c;
+    if (gs.n > 0) {
+        int sq = 0;
+        while (sq + 1 < gs.n && c >= gs.chk[sq + 1]) sq++;
+        cl = c - gs.chk[sq];
+        const int r0 = gs.tok[sq];
+        T = gs.tok[sq + 1] - r0;
+        q += (size_t)r0 * HK * DK;
+        k += (size_t)r0 * HK * DK;
+        v += (size_t)r0 * H * DK;
+        g += (size_t)r0 * H;
+        beta += (size_t)r0 * H;
+    }
+    const int hk = h / (H / HK);
+    const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool kside = wave < 4;
+    const int blk = wave & 3;  // k row block (k side) / q row block and v dim step (q side)
+    const size_t rec = (size_t)h * NC + c;
+    const int t0 = cl * C;
+
+    // 0. loads
+    const int row = 16 * blk + col;
+    u32x4 raw[4], vc[4];
+    {
+        const bf16* src = kside ? k : q;
+#pragma unroll
+        for (int s = 0; s < 4; s++) raw[s] = load_perm(src + ((size_t)(t0 + row) * HK + hk) * DK, s, grp, t0 + row < T);
+        if (!kside) {
+#pragma unroll
+            for (int tb_ = 0; tb_ < 4; tb_++) {
+                const int t = t0 + 16 * tb_ + col;
+                vc[tb_] = load_perm(v + ((size_t)t * H + h) * DK, blk, grp, t < T);
+            }
+        }
+    }
+    const int tl = t0 + lane;
+    const float gv = tl < T ? g[(size_t)tl * H + h] : 0.f;
+    const float bv = tl < T ? f32(beta[(size_t)tl * H + h]) : 0.f;
+
+    // 1. cumulative log-decay, in index order (every wave, lane = token)
+    float cs = 0.f;
+    for (int j = 0; j < C; j++) {
+        const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
+        if (j <= lane) cs = cs + gj;
+    }
+    const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs), C - 1));
+    const float ec = expf(cs), er = expf(last - cs);
+    if (wave == 0) {
+        cum[lane] = cs;
+        bet[lane] = bv;
+        ecum[lane] = ec;
+        erem[lane] = er;
+        if (lane == C - 1) ws.decay[rec] = expf(cs);
+    }
+
+    // 2. L2 norms and TF32 splits: k side -> k planes, q side -> q planes and qd
+    {
+        float ss = 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            float xf[8];
+            unpack8v(raw[s], xf);
+#pragma unroll
+            for (int e = 0; e < 8; e++) ss += xf[e] * xf[e];
+        }
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        if (kside) {
+            const float kinv = rsqrtf(ss + 1e-6f);
+            if (grp == 0) kinv_s[row] = kinv;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                float hk_[8], lk_[8], kf[8];
+                unpack8v(raw[s], kf);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float kt = tf32_rna(kf[e] * kinv);
+                    hk_[e] = round_bf16(kt);
+                    lk_[e] = kt - hk_[e];
+                }
+                khi_pl[(blk * 4 + s) * FRAG + lane] = pack8v(hk_);
+                klo_pl[(blk * 4 + s) * FRAG + lane] = pack8v(lk_);
+            }
+        } else {
+            const float qinv = rsqrtf(ss + 1e-6f) * scale;
+            const float ecq = __shfl(ec, row, 64);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                float hq_[8], lq_[8], qd_[8], qf[8];
+                unpack8v(raw[s], qf);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float qx = qf[e] * qinv;
+                    const float qt = tf32_rna(qx);
+                    hq_[e] = round_bf16(qt);
+                    lq_[e] = qt - hq_[e];
+                    qd_[e] = qx * ecq;
+                }
+                qhi_pl[(blk * 4 + s) * FRAG + lane] = pack8v(hq_);
+                qlo_pl[(blk * 4 + s) * FRAG + lane] = pack8v(lq_);
+                ws.qd[(rec * 16 + blk * 4 + s) * FRAG + lane] = pack8v(qd_);
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. pair products by table: 10 A tiles and the 8 pb fragments (two of them all zero: the
+    //    scan reads every fragment) over 8 waves
+    switch (wave) {
+        case 0:
+            prep8_a_tile(3, 3, khi_pl, klo_pl, am, cum, bet, lane);
+            prep8_a_tile(3, 2, khi_pl, klo_pl, am, cum, bet, lane);
+            prep8_a_tile(0, 0, khi_pl, klo_pl, am, cum, bet, lane);
+            break;
+        case 1:
+            prep8_a_tile(3, 1, khi_pl, klo_pl, am, cum, bet, lane);
+            prep8_a_tile(3, 0, khi_pl, klo_pl, am, cum, bet, lane);
+            prep8_a_tile(1, 1, khi_pl, klo_pl, am, cum, bet, lane);
+            break;
+        case 2:
+            prep8_a_tile(2, 2, khi_pl, klo_pl, am, cum, bet, lane);
+            prep8_a_tile(2, 1, khi_pl, klo_pl, am, cum, bet, lane);
+            prep8_a_tile(2, 0, khi_pl, klo_pl, am, cum, bet, lane);
+            break;
+        case 3:
+            prep8_a_tile(1, 0, khi_pl, klo_pl, am, cum, bet, lane);
+            prep8_p_frag(0, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+            break;
+        case 4:
+            prep8_p_frag(3, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+            prep8_p_frag(0, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);  // zeros
+            break;
+        case 5:
+            prep8_p_frag(3, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+            prep8_p_frag(1, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);  // zeros
+            break;
+        case 6:
+            prep8_p_frag(2, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+            prep8_p_frag(2, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+            break;
+        default:
+            prep8_p_frag(1, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+            break;
+    }
+    __syncthreads();
+
+    // 4. T = (I + A)^-1: zero upper blocks (all threads), diagonal blocks on waves 0-3
+    for (int x = tid; x < 6 * 256; x += PT8) {
+        const int blk_ = x / 256, r = (x % 256) / 16, cc = x % 16;
+        const int bi = blk_ < 3 ? 0 : blk_ < 5 ? 1 : 2;
+        const int bj = blk_ < 3 ? blk_ + 1 : blk_ < 5 ? blk_ - 1 : 3;
+        tm[(16 * bi + r) * FLD + 16 * bj + cc] = 0.f;
+    }
+    if (kside && lane < 16) {
+        const int base = 16 * blk, cc = lane;
+        float xs[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            float acc = r == cc ? 1.f : 0.f;
+#pragma unroll
+            for (int j = 0; j < r; j++) acc = fmaf(-am[(base + r) * FLD + base + j], xs[j], acc);
+            xs[r] = acc;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) tm[(base + r) * FLD + base + cc] = xs[r];
+    }
+    __syncthreads();
+    float* scr = reinterpret_cast<float*>(sm + R0_SC) + blk * 256;
+    for (int lv = 1; lv < 4; lv++) {
+        const int bi = blk, bj = blk - lv;
+        const bool active = kside && bj >= 0;
+        if (active) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            for (int kb = bj; kb < bi; kb++)
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++)
+                    acc = mfma_f32(am[(16 * bi + col) * FLD + 16 * kb + 4 * kk + grp],
+                                   tm[(16 * kb + 4 * kk + grp) * FLD + 16 * bj + col], acc);
+#pragma unroll
+            for (int r = 0; r < 4; r++) scr[(4 * grp + r) * 16 + col] = acc[r];
+        }
+        __syncthreads();
+        if (active) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+                acc = mfma_f32(tm[(16 * bi + col) * FLD + 16 * bi + 4 * kk + grp], scr[(4 * kk + grp) * 16 + col], acc);
+#pragma unroll
+            for (int r = 0; r < 4; r++) tm[(16 * bi + 4 * grp + r) * FLD + 16 * bj + col] = -acc[r];
+        }
+        __syncthreads();
+    }
+
+    // 5. Tb = bf16(T beta_j); the raw k rows go to region 1 (A is dead) for step 6
+    if (kside) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) reinterpret_cast<u32x4*>(am)[(blk * 4 + s) * FRAG + lane] = raw[s];
+    }
+    for (int x = tid; x < C * C; x += PT8) {
+        const int i = x / C, j = x % C;
+        tb[i * TLD + j] = to_bf16(tm[i * FLD + j] * bet[j]);
+    }
+    __syncthreads();
+
+    // 6. dim step ds = wave & 3: q side (waves 4-7) kd and v transposes, kd fragments and
+    //    u = Tb v; k side (waves 0-3) the kw transpose and w^T = kw^T Tb^T
+    const int ds = blk;
+    u32x4 f[2][2];  // fvt (q side) or fkw (k side) [token step][half]
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        f32x4 ta[2][2], tk[2][2];
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int tb_ = 2 * s + p, rw = 16 * tb_ + col;
+            const float ki = kinv_s[rw], e = kside ? ecum[rw] : erem[rw];
+            float kf[8], a[8];
+            unpack8v(reinterpret_cast<const u32x4*>(am)[(tb_ * 4 + ds) * FRAG + lane], kf);
+#pragma unroll
+            for (int x = 0; x < 8; x++) a[x] = kf[x] * ki * e;
+            const u32x4 ak = pack8v(a);
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const u32x4 sel = select_op(half, col, grp);
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                tk[p][half] = mfma16(ak, sel, z);
+                if (!kside) ta[p][half] = mfma16(vc[tb_], sel, z);
+            }
+        }
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            if (kside) {
+                f[s][half] = pack_pair(tk[0][half], tk[1][half]);
+            } else {
+                ws.kd[(rec * 16 + (2 * ds + half) * 2 + s) * FRAG + lane] = pack_pair(tk[0][half], tk[1][half]);
+                f[s][half] = pack_pair(ta[0][half], ta[1][half]);
+            }
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+        f32x4 wt[2];
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s <= it / 2; s++) {  // T is lower triangular
+                const bf16* tr = tb + (16 * it + col) * TLD + 32 * s + 4 * grp;
+                const u32x2 t_lo = *reinterpret_cast<const u32x2*>(tr);
+                const u32x2 t_hi = *reinterpret_cast<const u32x2*>(tr + 16);
+                const u32x4 tbf = u32x4{t_lo[0], t_lo[1], t_hi[0], t_hi[1]};
+                acc = kside ? mfma16(f[s][half], tbf, acc) : mfma16(tbf, f[s][half], acc);
+            }
+            if (!kside)
+                ws.u[(rec * 32 + it * 8 + 2 * ds + half) * FRAG + lane] =
+                    u32x2{pack2(acc[0], acc[1]), pack2(acc[2], acc[3])};
+            wt[half] = acc;
+        }
+        if (kside) ws.w[(rec * 16 + it * 4 + ds) * FRAG + lane] = pack_pair(wt[0], wt[1]);
+    }
+}
+
 // ------------------------------------------------------------------ gdn_scan
 
 constexpr int ST = 512;   // threads: waves 0-3 carry the state, waves 4-7 the output
@@ -805,6 +1155,31 @@ Plan plan_segments(int T, int H) {
     return p;
 }
 
+// CU count of the current device (looked up once per device).
+int device_cus() {
+    constexpr int MAX_DEV = 64;
+    static std::atomic<int> cus_of[MAX_DEV];  // 0: not looked up yet
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 0;
+    int n = cus_of[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+        cus_of[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// gdn_prep8 when every item gets a CU of its own (the launch is latency-bound); gdn_prep (three
+// 4-wave blocks per CU) otherwise. Overridable for tests by Q35_PREP_WIDE (0 or 1).
+bool prep_wide(long items) {
+    if (const char* e = getenv("Q35_PREP_WIDE")) {
+        if (e[0] == '0') return false;
+        if (e[0] == '1') return true;
+    }
+    const int cus = device_cus();
+    return cus > 0 && items <= cus;
+}
+
 // Halves per scan block: one 8-wave scan block fits a CU, so `units` (heads x sequences)
 // blocks of NSUB halves run in ceil(units * 8 / NSUB / CUs) rounds. The two-half block's chunk
 // step is ~1.46x the one-half block's (measured alone on the device: 1.24 vs 0.85 us), so it
@@ -815,16 +1190,8 @@ int scan_halves(int units) {
         const int v = atoi(e);
         if (v == 1 || v == 2) return v;
     }
-    constexpr int MAX_DEV = 64;
-    static std::atomic<int> cus_of[MAX_DEV];  // 0: not looked up yet
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 1;
-    int n = cus_of[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 1;
-        cus_of[dev].store(n, std::memory_order_relaxed);
-    }
-    const long cus = n;
+    const long cus = device_cus();
+    if (cus <= 0) return 1;
     const long r1 = ((long)units * 8 + cus - 1) / cus, r2 = ((long)units * 4 + cus - 1) / cus;
     return 146 * r2 < 100 * r1 ? 2 : 1;
 }
@@ -847,9 +1214,18 @@ int gdn_launch(const void* q, const void* k, const void* v, const float* g, cons
     }
     if (NC == 0) return hipSuccess;
     const Work ws = split(workspace, NC, H);
-    gdn_prep<<<dim3(NC, H), PT, PREP_SMEM, st>>>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
-                                                 static_cast<const bf16*>(v), g, static_cast<const bf16*>(beta), ws, T,
-                                                 H, HK, scale, gs);
+    if (prep_wide((long)NC * H)) {
+        static const hipError_t configured8 = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(gdn_prep8), hipFuncAttributeMaxDynamicSharedMemorySize, PREP8_SMEM);
+        if (configured8 != hipSuccess) return configured8;
+        gdn_prep8<<<dim3(NC, H), PT8, PREP8_SMEM, st>>>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                                                        static_cast<const bf16*>(v), g, static_cast<const bf16*>(beta),
+                                                        ws, T, H, HK, scale, gs);
+    } else {
+        gdn_prep<<<dim3(NC, H), PT, PREP_SMEM, st>>>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                                                     static_cast<const bf16*>(v), g, static_cast<const bf16*>(beta), ws,
+                                                     T, H, HK, scale, gs);
+    }
     const int halves = scan_halves(H * nseq);
     auto scan = halves == 2 ? gdn_scan<2> : gdn_scan<1>;
     scan<<<H * (DK / (BV * halves)) * nseq, ST, 0, st>>>(ws, ws.decay, static_cast<bf16*>(o), T, H, NC,
