@@ -507,6 +507,8 @@ __global__ void __launch_bounds__(PT)
 // all fit on the device at once (one block per CU), where a block's latency sets the time:
 //   * waves 0-3 load and normalise k row block `wave`, waves 4-7 q row block `wave - 4` (and the
 //     v columns of dim step `wave - 4`); both sides write their TF32 planes to LDS;
+//   * the cumulative log-decay runs on wave 3 alone and reaches the others through LDS; the q
+//     side forms qd after the barrier that publishes it;
 //   * the ten A tiles and the six pb fragments (ten P tiles) go to the eight waves by a fixed
 //     table, two or three tiles each, both operands from the LDS planes;
 //   * the inverse runs on waves 0-3 as in gdn_prep;
@@ -626,27 +628,29 @@ __global__ void __launch_bounds__(PT8)
             }
         }
     }
-    const int tl = t0 + lane;
-    const float gv = tl < T ? g[(size_t)tl * H + h] : 0.f;
-    const float bv = tl < T ? f32(beta[(size_t)tl * H + h]) : 0.f;
 
-    // 1. cumulative log-decay, in index order (every wave, lane = token)
-    float cs = 0.f;
-    for (int j = 0; j < C; j++) {
-        const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
-        if (j <= lane) cs = cs + gj;
-    }
-    const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs), C - 1));
-    const float ec = expf(cs), er = expf(last - cs);
-    if (wave == 0) {
+    // 1. cumulative log-decay on wave 3 alone (lane = token), published through LDS for step
+    //    3 on: one chain of 64 dependent adds in index order, lane j keeping the running sum
+    //    after term j (the same additions in the same order as a per-lane prefix loop)
+    if (wave == 3) {
+        const int tl = t0 + lane;
+        const float gv = tl < T ? g[(size_t)tl * H + h] : 0.f;
+        const float bv = tl < T ? f32(beta[(size_t)tl * H + h]) : 0.f;
+        float run = 0.f, cs = 0.f;
+#pragma unroll
+        for (int j = 0; j < C; j++) {
+            run = run + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
+            cs = lane == j ? run : cs;
+        }
         cum[lane] = cs;
         bet[lane] = bv;
-        ecum[lane] = ec;
-        erem[lane] = er;
+        ecum[lane] = expf(cs);
+        erem[lane] = expf(run - cs);
         if (lane == C - 1) ws.decay[rec] = expf(cs);
     }
 
-    // 2. L2 norms and TF32 splits: k side -> k planes, q side -> q planes and qd
+    // 2. L2 norms and TF32 splits: k side -> k planes, q side -> q planes
+    float qinv = 0.f;
     {
         float ss = 0.f;
 #pragma unroll
@@ -675,27 +679,35 @@ __global__ void __launch_bounds__(PT8)
                 klo_pl[(blk * 4 + s) * FRAG + lane] = pack8v(lk_);
             }
         } else {
-            const float qinv = rsqrtf(ss + 1e-6f) * scale;
-            const float ecq = __shfl(ec, row, 64);
+            qinv = rsqrtf(ss + 1e-6f) * scale;
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                float hq_[8], lq_[8], qd_[8], qf[8];
+                float hq_[8], lq_[8], qf[8];
                 unpack8v(raw[s], qf);
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
-                    const float qx = qf[e] * qinv;
-                    const float qt = tf32_rna(qx);
+                    const float qt = tf32_rna(qf[e] * qinv);
                     hq_[e] = round_bf16(qt);
                     lq_[e] = qt - hq_[e];
-                    qd_[e] = qx * ecq;
                 }
                 qhi_pl[(blk * 4 + s) * FRAG + lane] = pack8v(hq_);
                 qlo_pl[(blk * 4 + s) * FRAG + lane] = pack8v(lq_);
-                ws.qd[(rec * 16 + blk * 4 + s) * FRAG + lane] = pack8v(qd_);
             }
         }
     }
     __syncthreads();
+    // qd = (q^ scale) e^cum once the cumulative decay is in LDS
+    if (!kside) {
+        const float ecq = ecum[row];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            float qd_[8], qf[8];
+            unpack8v(raw[s], qf);
+#pragma unroll
+            for (int e = 0; e < 8; e++) qd_[e] = qf[e] * qinv * ecq;
+            ws.qd[(rec * 16 + blk * 4 + s) * FRAG + lane] = pack8v(qd_);
+        }
+    }
 
     // 3. pair products by table: 10 A tiles and the 8 pb fragments (two of them all zero: the
     //    scan reads every fragment) over 8 waves
@@ -1032,21 +1044,28 @@ __global__ void __launch_bounds__(ST)
         // four rotating operand sets: chunk c + 3 is requested while chunk c is processed
         ChainOps<NSUB> opa, opb, opc, opd;
         load_chain(opa, sr, decay, at(0), rb, lane, slice);
+        __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits count whole sets
         load_chain(opb, sr, decay, at(1), rb, lane, slice);
+        __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits count whole sets
         load_chain(opc, sr, decay, at(2), rb, lane, slice);
-        for (int c = 0; c < NC; c += 4) {
+        // Whole groups of four chunks, then a tail of at most three. The main loop has no
+        // early exit, so its only back edge follows the fourth step and the compiler's memory
+        // waits stay per operand set (an exit after the first step would merge into the loop
+        // header and make every group wait for the loads of the two newest sets).
+        const int NC4 = NC & ~3;
+        for (int c = 0; c < NC4; c += 4) {
             load_chain(opd, sr, decay, at(c + 3), rb, lane, slice);
             step(opa);
-            if (c + 1 >= NC) break;
             load_chain(opa, sr, decay, at(c + 4), rb, lane, slice);
             step(opb);
-            if (c + 2 >= NC) break;
             load_chain(opb, sr, decay, at(c + 5), rb, lane, slice);
             step(opc);
-            if (c + 3 >= NC) break;
             load_chain(opc, sr, decay, at(c + 6), rb, lane, slice);
             step(opd);
         }
+        if (NC4 < NC) step(opa);
+        if (NC4 + 1 < NC) step(opb);
+        if (NC4 + 2 < NC) step(opc);
         Q35_LPHASE_FLUSH();
         if (s_out) {
 #pragma unroll
@@ -1094,21 +1113,24 @@ __global__ void __launch_bounds__(ST)
         };
         OutOps opa, opb, opc, opd;
         load_out(opa, sr, at(0), rb, lane);
+        __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits count whole sets
         load_out(opb, sr, at(1), rb, lane);
+        __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits count whole sets
         load_out(opc, sr, at(2), rb, lane);
-        for (int c = 0; c < NC; c += 4) {
+        const int NC4 = NC & ~3;  // the same group / tail split as the chain waves
+        for (int c = 0; c < NC4; c += 4) {
             load_out(opd, sr, at(c + 3), rb, lane);
             step(opa, c);
-            if (c + 1 >= NC) break;
             load_out(opa, sr, at(c + 4), rb, lane);
             step(opb, c + 1);
-            if (c + 2 >= NC) break;
             load_out(opb, sr, at(c + 5), rb, lane);
             step(opc, c + 2);
-            if (c + 3 >= NC) break;
             load_out(opc, sr, at(c + 6), rb, lane);
             step(opd, c + 3);
         }
+        if (NC4 < NC) step(opa, NC4);
+        if (NC4 + 1 < NC) step(opb, NC4 + 1);
+        if (NC4 + 2 < NC) step(opc, NC4 + 2);
     }
 }
 
