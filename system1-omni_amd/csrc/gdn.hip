@@ -520,6 +520,21 @@ constexpr int PT8 = 512;
 constexpr int QPL = PREP_SMEM;                         // q^ planes: hi then lo, [4 blocks][4 steps]
 constexpr int PREP8_SMEM = QPL + 2 * PLANE;
 
+// One fragment (64 lanes x 16 or 8 bytes at frag, a wave-uniform address) stored at device
+// scope (the SC1 cache-policy bit): the line is written through the XCD's L2 instead of being
+// left dirty there. A kernel's end writes back every dirty L2 line before the next kernel can
+// start, and for the 8-wave prep, whose records (72 KB per item) are all written in the last
+// microseconds of the launch, that flush was the largest part of the gap before the scan
+// (config 0: 5.4 us with ~9 MB of records, 1.9 us with them written through). The 4-wave prep
+// keeps ordinary stores: its records are re-read by the scan of the same segment from L2.
+template <typename V>
+__device__ __forceinline__ void store_through(V* frag, int lane, V v) {
+    const auto r = __builtin_amdgcn_make_buffer_rsrc(frag, (short)0, 0x7fffffff, 0x00020000);
+    constexpr int SC1 = 0x10;
+    if constexpr (sizeof(V) == 16) __builtin_amdgcn_raw_buffer_store_b128(v, r, lane * 16, 0, SC1);
+    else __builtin_amdgcn_raw_buffer_store_b64(v, r, lane * 8, 0, SC1);
+}
+
 // A tile (i, j) of the chunk: A_ij for the rows of k block i and the columns of k block j
 __device__ __forceinline__ void prep8_a_tile(int bi, int bj, const u32x4* khi_pl, const u32x4* klo_pl, float* am,
                                              const float* cum, const float* bet, int lane) {
@@ -570,7 +585,7 @@ __device__ __forceinline__ void prep8_p_frag(int qb, int s2, const u32x4* khi_pl
             pt[p][r] = j <= i ? round_bf16(pt[p][r] * expf(cum[i] - cum[j])) : 0.f;
         }
     }
-    ws.pb[(rec * 8 + qb * 2 + s2) * FRAG + lane] = pack_pair(pt[0], pt[1]);
+    store_through(&ws.pb[(rec * 8 + qb * 2 + s2) * FRAG], lane, pack_pair(pt[0], pt[1]));
 }
 
 __global__ void __launch_bounds__(PT8)
@@ -705,7 +720,7 @@ __global__ void __launch_bounds__(PT8)
             unpack8v(raw[s], qf);
 #pragma unroll
             for (int e = 0; e < 8; e++) qd_[e] = qf[e] * qinv * ecq;
-            ws.qd[(rec * 16 + blk * 4 + s) * FRAG + lane] = pack8v(qd_);
+            store_through(&ws.qd[(rec * 16 + blk * 4 + s) * FRAG], lane, pack8v(qd_));
         }
     }
 
@@ -836,7 +851,7 @@ __global__ void __launch_bounds__(PT8)
             if (kside) {
                 f[s][half] = pack_pair(tk[0][half], tk[1][half]);
             } else {
-                ws.kd[(rec * 16 + (2 * ds + half) * 2 + s) * FRAG + lane] = pack_pair(tk[0][half], tk[1][half]);
+                store_through(&ws.kd[(rec * 16 + (2 * ds + half) * 2 + s) * FRAG], lane, pack_pair(tk[0][half], tk[1][half]));
                 f[s][half] = pack_pair(ta[0][half], ta[1][half]);
             }
         }
@@ -856,11 +871,11 @@ __global__ void __launch_bounds__(PT8)
                 acc = kside ? mfma16(f[s][half], tbf, acc) : mfma16(tbf, f[s][half], acc);
             }
             if (!kside)
-                ws.u[(rec * 32 + it * 8 + 2 * ds + half) * FRAG + lane] =
-                    u32x2{pack2(acc[0], acc[1]), pack2(acc[2], acc[3])};
+                store_through(&ws.u[(rec * 32 + it * 8 + 2 * ds + half) * FRAG], lane,
+                              u32x2{pack2(acc[0], acc[1]), pack2(acc[2], acc[3])});
             wt[half] = acc;
         }
-        if (kside) ws.w[(rec * 16 + it * 4 + ds) * FRAG + lane] = pack_pair(wt[0], wt[1]);
+        if (kside) store_through(&ws.w[(rec * 16 + it * 4 + ds) * FRAG], lane, pack_pair(wt[0], wt[1]));
     }
 }
 
