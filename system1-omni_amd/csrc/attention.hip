@@ -491,8 +491,9 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
 // from global memory straight into LDS (buffer_load_dwordx4 ... lds, no registers, no LDS
 // stores): K and V keep their row-major layout, 16-byte chunks permuted within each row so
 // fragment reads spread over the banks, and V^T fragments come out of ds_read_b64_tr_b16.
-// The four partial softmax states are merged through LDS, each key group finishing one
-// 32-dim slice of the output. Tile boundaries are fixed multiples of 32 from key 0 and the
+// The two key groups' partial softmax states are merged through LDS: a wave publishes the
+// half of its output the other group finishes and merges its own half from registers, each
+// group finishing 64 dims. Tile boundaries are fixed multiples of 32 from key 0 and the
 // merge order is fixed, so a row's arithmetic does not depend on its block (windowed and
 // packed launches repeat the full pass bit for bit).
 namespace fa32 {
@@ -503,9 +504,9 @@ constexpr int NSTAGE = 4;                  // LDS stages per key group
 constexpr int ROW = 256;                   // bytes per K or V row (128 bf16)
 constexpr int K_BYTES = BN * ROW;          // 8192
 constexpr int STAGE = 2 * K_BYTES;         // one K tile and one V tile
-constexpr int PART = 66;                   // floats per lane of a partial state: o (64), m, l
-constexpr int BYTES = 8 * PART * 64 * 4;   // the merge area (135168) covers 2 groups x 4 stages
-static_assert(KG * NSTAGE * STAGE <= BYTES, "stages must fit");
+constexpr int XS = 36;                     // floats per lane of a published half state: o (32), m, l, pad
+constexpr int BYTES = KG * NSTAGE * STAGE;  // the stages (131072); the exchange reuses them
+static_assert(8 * 64 * XS * 4 <= BYTES, "the exchange fits in the stages");
 // s_waitcnt with at most 8 vector memory operations outstanding (a wave issues four
 // transfers per step): vmcnt 8 (bits 3:0 = 8, bits 15:14 = 0), lgkmcnt and expcnt untouched
 constexpr int VMCNT_TWO_STEPS = 0x0f78;
@@ -818,53 +819,68 @@ __global__ void __launch_bounds__(512, 1)
 #pragma unroll
         for (int j = 0; j < 8; j++) gp[j] = *reinterpret_cast<const u32x2*>(gate + orow + 8 * j);
     }
-    float* part = reinterpret_cast<float*>(smem);
-    {
-        float* pp = part + wave * PART * 64 + lane;
+    // Exchange: each wave publishes the half of its partial output the other key group
+    // finishes (o[2 (1 - kg)], o[2 (1 - kg) + 1]) and its m and l, lane-contiguous (XS floats
+    // per lane: 16-byte accesses, conflict-free), and merges its own half from registers.
+    float* xch = reinterpret_cast<float*>(smem);
+    auto finish = [&](auto kgc) {
+        constexpr int K = decltype(kgc)::value;  // this wave's key group
+        {
+            f32x4* px = reinterpret_cast<f32x4*>(xch + (wave * 64 + lane) * XS);
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) pp[(16 * t + i) * 64] = o[t][i];
-        pp[64 * 64] = m;
-        pp[65 * 64] = l;
-    }
-    __syncthreads();
-    float mk[KG], ak[KG];
-    float mm = -INFINITY;
-#pragma unroll
-    for (int g = 0; g < KG; g++) {
-        mk[g] = part[((4 * g + gw) * PART + 64) * 64 + lane];
-        mm = fmaxf(mm, mk[g]);
-    }
-    const float base = mm == -INFINITY ? 0.f : mm;
-    float lt = 0.f;
-#pragma unroll
-    for (int g = 0; g < KG; g++) {
-        ak[g] = __builtin_amdgcn_exp2f(mk[g] - base);
-        lt += part[((4 * g + gw) * PART + 65) * 64 + lane] * ak[g];
-    }
-    lt += __shfl_xor(lt, 32, 64);
-    if (qrow >= T) return;
-    const float inv = 1.f / lt;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        float a[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float acc = 0.f;
-#pragma unroll
-            for (int g = 0; g < KG; g++) acc += part[((4 * g + gw) * PART + 32 * kg + 4 * j + r) * 64 + lane] * ak[g];
-            a[r] = acc * inv;
+                for (int q4 = 0; q4 < 4; q4++)
+                    px[4 * t + q4] = f32x4{o[2 * (1 - K) + t][4 * q4], o[2 * (1 - K) + t][4 * q4 + 1],
+                                          o[2 * (1 - K) + t][4 * q4 + 2], o[2 * (1 - K) + t][4 * q4 + 3]};
+            px[8] = f32x4{m, l, 0.f, 0.f};
         }
-        if (GATED) {
-            a[0] = round_bf16(a[0]) * round_bf16(gate_sigmoid(lo_f32(gp[j][0])));
-            a[1] = round_bf16(a[1]) * round_bf16(gate_sigmoid(hi_f32(gp[j][0])));
-            a[2] = round_bf16(a[2]) * round_bf16(gate_sigmoid(lo_f32(gp[j][1])));
-            a[3] = round_bf16(a[3]) * round_bf16(gate_sigmoid(hi_f32(gp[j][1])));
+        __syncthreads();
+        const f32x4* qx = reinterpret_cast<const f32x4*>(xch + ((4 * (1 - K) + gw) * 64 + lane) * XS);
+        const f32x4 pml = qx[8];
+        const float mk[KG] = {K == 0 ? m : pml[0], K == 0 ? pml[0] : m};
+        const float lk[KG] = {K == 0 ? l : pml[1], K == 0 ? pml[1] : l};
+        float ak[KG];
+        float mm = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < KG; g++) mm = fmaxf(mm, mk[g]);
+        const float base = mm == -INFINITY ? 0.f : mm;
+        float lt = 0.f;
+#pragma unroll
+        for (int g = 0; g < KG; g++) {
+            ak[g] = __builtin_amdgcn_exp2f(mk[g] - base);
+            lt += lk[g] * ak[g];
         }
-        *reinterpret_cast<u32x2*>(out + orow + 8 * j) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
-    }
-    if (lse != nullptr && kg == 0 && hh == 0) lse[(size_t)h * lse_ld + qrow] = (mm + log2f(lt)) * 0.69314718055994531f;
+        lt += __shfl_xor(lt, 32, 64);
+        if (qrow >= T) return;
+        const float inv = 1.f / lt;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const f32x4 pv = qx[j];  // the other group's values of dims 64 K + 8 j + 4 hh + r
+            float a[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float mine = o[2 * K + j / 4][4 * (j % 4) + r];
+                const float p0 = K == 0 ? mine : pv[r], p1 = K == 0 ? pv[r] : mine;
+                float acc = 0.f;
+                acc += p0 * ak[0];
+                acc += p1 * ak[1];
+                a[r] = acc * inv;
+            }
+            if (GATED) {
+                a[0] = round_bf16(a[0]) * round_bf16(gate_sigmoid(lo_f32(gp[j][0])));
+                a[1] = round_bf16(a[1]) * round_bf16(gate_sigmoid(hi_f32(gp[j][0])));
+                a[2] = round_bf16(a[2]) * round_bf16(gate_sigmoid(lo_f32(gp[j][1])));
+                a[3] = round_bf16(a[3]) * round_bf16(gate_sigmoid(hi_f32(gp[j][1])));
+            }
+            *reinterpret_cast<u32x2*>(out + orow + 8 * j) = u32x2{pack2(a[0], a[1]), pack2(a[2], a[3])};
+        }
+        if (lse != nullptr && K == 0 && hh == 0) lse[(size_t)h * lse_ld + qrow] = (mm + log2f(lt)) * 0.69314718055994531f;
+    };
+    if (kg == 0)
+        finish(std::integral_constant<int, 0>{});
+    else
+        finish(std::integral_constant<int, 1>{});
 }
 
 template <bool GATED, bool PREFIX>
