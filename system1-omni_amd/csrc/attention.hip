@@ -486,8 +486,9 @@ __global__ void __launch_bounds__(FA_THREADS, 1)
 // flash32_kernel: the Dh = 128 GQA path (q heads per kv head a multiple of 4) on the
 // 32x32x16 MFMA (v_mfma_f32_32x32x16_bf16). A wave owns 16 query rows of two q heads (32
 // query columns), so one K or V fragment read from LDS feeds a 32x32 output tile. A block
-// owns 16 rows of the four q heads of one GQA group; its eight waves are 2 head pairs x 4 key
-// groups, group g taking the 32-key tiles g, g + 4, ... of the block's key range. Tiles move
+// owns 32 rows of the four q heads of one GQA group; its eight waves are 2 key groups x 2 row
+// halves x 2 head pairs, group g taking the 32-key tiles g, g + 2, ... of the block's key
+// range through its own four LDS stages. Tiles move
 // from global memory straight into LDS (buffer_load_dwordx4 ... lds, no registers, no LDS
 // stores): K and V keep their row-major layout, 16-byte chunks permuted within each row so
 // fragment reads spread over the banks, and V^T fragments come out of ds_read_b64_tr_b16.
