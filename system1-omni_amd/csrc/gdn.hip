@@ -512,8 +512,12 @@ __global__ void __launch_bounds__(PT)
 //   * the ten A tiles and the six pb fragments (ten P tiles) go to the eight waves by a fixed
 //     table, two or three tiles each, both operands from the LDS planes;
 //   * the inverse runs on waves 0-3 as in gdn_prep;
-//   * step 6 splits by product: waves 4-7 transpose v and kd and form u = Tb v (and the kd
-//     fragments), waves 0-3 transpose kw and form w^T, each for dim step `wave & 3`.
+//   * step 6 splits by product: waves 4-7 transpose v and kd (and store the kd fragments)
+//     while waves 0-3 work through the inverse's off-diagonal levels, then form u = Tb v;
+//     waves 0-3 transpose kw and form w^T, each for dim step `wave & 3`. The raw k rows for
+//     the transposes go to the q-plane region, free after the pair products;
+//   * an inverse level's partial product passes through the wave's own LDS scratch without
+//     a block barrier.
 // Every tile, fragment and store is computed by the same instruction sequence on the same
 // values as in gdn_prep, so the records are bit for bit the same.
 constexpr int PT8 = 512;
@@ -764,13 +768,57 @@ __global__ void __launch_bounds__(PT8)
     }
     __syncthreads();
 
-    // 4. T = (I + A)^-1: zero upper blocks (all threads), diagonal blocks on waves 0-3
+    // 4. T = (I + A)^-1: zero upper blocks (all threads), diagonal blocks on waves 0-3. The raw
+    //    k rows go to the q-plane region (dead after step 3) for step 6's transposes, which the
+    //    q side runs while waves 0-3 work through the off-diagonal levels.
+    u32x4* const kraw_pl = reinterpret_cast<u32x4*>(sm + QPL);
+    if (kside) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) kraw_pl[(blk * 4 + s) * FRAG + lane] = raw[s];
+    }
     for (int x = tid; x < 6 * 256; x += PT8) {
         const int blk_ = x / 256, r = (x % 256) / 16, cc = x % 16;
         const int bi = blk_ < 3 ? 0 : blk_ < 5 ? 1 : 2;
         const int bj = blk_ < 3 ? blk_ + 1 : blk_ < 5 ? blk_ - 1 : 3;
         tm[(16 * bi + r) * FLD + 16 * bj + cc] = 0.f;
     }
+    // step 6's transposes of dim step ds = wave & 3: q side the kd fragments (stored) and v,
+    // k side kw, into f[token step][half] (fvt or fkw)
+    const int ds = blk;
+    u32x4 f[2][2];
+    auto transposes = [&]() {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            f32x4 ta[2][2], tk[2][2];
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const int tb_ = 2 * s + p, rw = 16 * tb_ + col;
+                const float ki = kinv_s[rw], e = kside ? ecum[rw] : erem[rw];
+                float kf[8], a[8];
+                unpack8v(kraw_pl[(tb_ * 4 + ds) * FRAG + lane], kf);
+#pragma unroll
+                for (int x = 0; x < 8; x++) a[x] = kf[x] * ki * e;
+                const u32x4 ak = pack8v(a);
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    const u32x4 sel = select_op(half, col, grp);
+                    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    tk[p][half] = mfma16(ak, sel, z);
+                    if (!kside) ta[p][half] = mfma16(vc[tb_], sel, z);
+                }
+            }
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                if (kside) {
+                    f[s][half] = pack_pair(tk[0][half], tk[1][half]);
+                } else {
+                    store_through(&ws.kd[(rec * 16 + (2 * ds + half) * 2 + s) * FRAG], lane,
+                                  pack_pair(tk[0][half], tk[1][half]));
+                    f[s][half] = pack_pair(ta[0][half], ta[1][half]);
+                }
+            }
+        }
+    };
     if (kside && lane < 16) {
         const int base = 16 * blk, cc = lane;
         float xs[16];
@@ -785,6 +833,7 @@ __global__ void __launch_bounds__(PT8)
         for (int r = 0; r < 16; r++) tm[(base + r) * FLD + base + cc] = xs[r];
     }
     __syncthreads();
+    if (!kside) transposes();
     float* scr = reinterpret_cast<float*>(sm + R0_SC) + blk * 256;
     for (int lv = 1; lv < 4; lv++) {
         const int bi = blk, bj = blk - lv;
@@ -799,7 +848,7 @@ __global__ void __launch_bounds__(PT8)
 #pragma unroll
             for (int r = 0; r < 4; r++) scr[(4 * grp + r) * 16 + col] = acc[r];
         }
-        __syncthreads();
+        // scr is this wave's own: its writes precede its reads in the wave's LDS order
         if (active) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -811,51 +860,16 @@ __global__ void __launch_bounds__(PT8)
         __syncthreads();
     }
 
-    // 5. Tb = bf16(T beta_j); the raw k rows go to region 1 (A is dead) for step 6
-    if (kside) {
-#pragma unroll
-        for (int s = 0; s < 4; s++) reinterpret_cast<u32x4*>(am)[(blk * 4 + s) * FRAG + lane] = raw[s];
-    }
+    // 5. Tb = bf16(T beta_j)
     for (int x = tid; x < C * C; x += PT8) {
         const int i = x / C, j = x % C;
         tb[i * TLD + j] = to_bf16(tm[i * FLD + j] * bet[j]);
     }
     __syncthreads();
 
-    // 6. dim step ds = wave & 3: q side (waves 4-7) kd and v transposes, kd fragments and
-    //    u = Tb v; k side (waves 0-3) the kw transpose and w^T = kw^T Tb^T
-    const int ds = blk;
-    u32x4 f[2][2];  // fvt (q side) or fkw (k side) [token step][half]
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-        f32x4 ta[2][2], tk[2][2];
-#pragma unroll
-        for (int p = 0; p < 2; p++) {
-            const int tb_ = 2 * s + p, rw = 16 * tb_ + col;
-            const float ki = kinv_s[rw], e = kside ? ecum[rw] : erem[rw];
-            float kf[8], a[8];
-            unpack8v(reinterpret_cast<const u32x4*>(am)[(tb_ * 4 + ds) * FRAG + lane], kf);
-#pragma unroll
-            for (int x = 0; x < 8; x++) a[x] = kf[x] * ki * e;
-            const u32x4 ak = pack8v(a);
-#pragma unroll
-            for (int half = 0; half < 2; half++) {
-                const u32x4 sel = select_op(half, col, grp);
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                tk[p][half] = mfma16(ak, sel, z);
-                if (!kside) ta[p][half] = mfma16(vc[tb_], sel, z);
-            }
-        }
-#pragma unroll
-        for (int half = 0; half < 2; half++) {
-            if (kside) {
-                f[s][half] = pack_pair(tk[0][half], tk[1][half]);
-            } else {
-                store_through(&ws.kd[(rec * 16 + (2 * ds + half) * 2 + s) * FRAG], lane, pack_pair(tk[0][half], tk[1][half]));
-                f[s][half] = pack_pair(ta[0][half], ta[1][half]);
-            }
-        }
-    }
+    // 6. u = Tb v on the q side (its transposes ran in step 4); on the k side the kw transpose
+    //    and w^T = kw^T Tb^T
+    if (kside) transposes();
 #pragma unroll
     for (int it = 0; it < 4; it++) {
         f32x4 wt[2];
