@@ -420,7 +420,7 @@ __global__ void __launch_bounds__(PT)
 #pragma unroll
             for (int r = 0; r < 4; r++) scr[(4 * grp + r) * 16 + col] = acc[r];
         }
-        __syncthreads();
+        // scr is this wave's own: its writes precede its reads in the wave's LDS order
         if (active) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
