@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "qwen3_5_ops.h"
 
 namespace q35 {
@@ -103,5 +105,19 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 c)
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
 inline unsigned cdiv(size_t n, unsigned d) { return (unsigned)((n + d - 1) / d); }
+
+// CU count of the current device (looked up once per device; 0 if it cannot be read).
+inline int device_cus() {
+    constexpr int MAX_DEV = 64;
+    static std::atomic<int> cus_of[MAX_DEV];  // 0: not looked up yet
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 0;
+    int n = cus_of[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+        cus_of[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
 
 }  // namespace q35

@@ -1206,20 +1206,6 @@ Plan plan_segments(int T, int H) {
     return p;
 }
 
-// CU count of the current device (looked up once per device).
-int device_cus() {
-    constexpr int MAX_DEV = 64;
-    static std::atomic<int> cus_of[MAX_DEV];  // 0: not looked up yet
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return 0;
-    int n = cus_of[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
-        cus_of[dev].store(n, std::memory_order_relaxed);
-    }
-    return n;
-}
-
 // gdn_prep8 when every item gets a CU of its own (the launch is latency-bound); gdn_prep (three
 // 4-wave blocks per CU) otherwise. Overridable for tests by Q35_PREP_WIDE (0 or 1).
 bool prep_wide(long items) {
