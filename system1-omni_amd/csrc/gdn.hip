@@ -32,7 +32,8 @@
 //       - every scan operand is written to the workspace in the exact per-lane order the
 //         scan's MFMA consumes it (1 KB per wave per store, fully coalesced).
 //   * gdn_scan, grid (head x 8 slices of 16 value columns, or x 4 slices of 32 when that
-//     needs fewer rounds of blocks), 4 chain waves + 4 output waves.  The float32 state
+//     needs fewer rounds of blocks), 4 chain waves + 4 output waves (16-column slices: two
+//     sets of 4 output waves taking alternate chunks).  The float32 state
 //     slice 128 x 16 (per half) lives in MFMA accumulators; each chunk streams its operand
 //     fragments from HBM/L2 straight into registers (three chunks ahead) and exchanges only
 //     bf16(S) and v_new through LDS.  The output o = qd Sb + pb v_new is produced in the
@@ -895,7 +896,6 @@ __global__ void __launch_bounds__(PT8)
 
 // ------------------------------------------------------------------ gdn_scan
 
-constexpr int ST = 512;   // threads: waves 0-3 carry the state, waves 4-7 the output
 constexpr int BV = 16;    // value columns per MFMA tile; a block owns NSUB such halves
 constexpr int SLD = DK + 8;  // bf16 stride of Sb^T [16 NSUB][128]
 constexpr int VLD = C + 8;   // bf16 stride of v_new^T [16 NSUB][64]
@@ -971,14 +971,20 @@ __device__ __forceinline__ u32x4 lds_perm(const bf16* base, int ld, int col, int
 // on the same operand fragments as a one-half block would, so both forms give the same bits;
 // the two-half form fetches each chunk's shared w / kd / qd / pb fragments once for two halves
 // and is used when it needs fewer rounds of blocks on the device (gdn_launch).
-template <int NSUB>
-__global__ void __launch_bounds__(ST)
+//
+// OS = 2: two sets of four output waves (12 waves), set X taking the chunks c with c % 2 == X.
+// bf16(S) and v_new are double-buffered by chunk parity, so a set reads chunk c's copies after
+// barriers A and B of chunk c and has the two barrier windows of chunk c + 1 for its o stores
+// and operand prefetches, which no longer hold the chain waves at the next barrier A. The
+// products are the same instructions on the same operands, so the output is the same bits.
+template <int NSUB, int OS>
+__global__ void __launch_bounds__(256 + 256 * OS)
     gdn_scan(Work ws, const float* __restrict__ decay_all, bf16* __restrict__ o, int T, int H, int NC,
              const float* __restrict__ s_in, size_t s_in_stride, float* __restrict__ s_out, size_t s_out_stride,
              const GSeqs gs) {
     constexpr int BVB = BV * NSUB, NSB = DK / BVB;
-    __shared__ __align__(16) bf16 sbt[BVB * SLD];
-    __shared__ __align__(16) bf16 vnt[BVB * VLD];
+    __shared__ __align__(16) bf16 sbt_[OS][BVB * SLD];
+    __shared__ __align__(16) bf16 vnt_[OS][BVB * VLD];
     const int h = blockIdx.x % H, slice = (blockIdx.x / H) % NSB, v0 = slice * BVB;
     size_t rec0 = (size_t)h * NC;
     if (gs.n > 0) {
@@ -1024,7 +1030,9 @@ __global__ void __launch_bounds__(ST)
                     st[hf][i][r] = s_in ? s_in[((size_t)h * DK + 32 * rb + 16 * i + 4 * grp + r) * DK + v0 + 16 * hf + col]
                                         : 0.f;
         Q35_LPHASE_START();
-        auto step = [&](const ChainOps<NSUB>& cur) {
+        auto step = [&](const ChainOps<NSUB>& cur, int par) {
+            bf16* sbt = sbt_[OS == 2 ? par : 0];
+            bf16* vnt = vnt_[OS == 2 ? par : 0];
 #pragma unroll
             for (int hf = 0; hf < NSUB; hf++)
 #pragma unroll
@@ -1070,31 +1078,51 @@ __global__ void __launch_bounds__(ST)
                 }
             Q35_LPHASE(12);
         };
-        // four rotating operand sets: chunk c + 3 is requested while chunk c is processed
-        ChainOps<NSUB> opa, opb, opc, opd;
-        load_chain(opa, sr, decay, at(0), rb, lane, slice);
-        __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits count whole sets
-        load_chain(opb, sr, decay, at(1), rb, lane, slice);
-        __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits count whole sets
-        load_chain(opc, sr, decay, at(2), rb, lane, slice);
-        // Whole groups of four chunks, then a tail of at most three. The main loop has no
-        // early exit, so its only back edge follows the fourth step and the compiler's memory
-        // waits stay per operand set (an exit after the first step would merge into the loop
-        // header and make every group wait for the loads of the two newest sets).
-        const int NC4 = NC & ~3;
-        for (int c = 0; c < NC4; c += 4) {
-            load_chain(opd, sr, decay, at(c + 3), rb, lane, slice);
-            step(opa);
-            load_chain(opa, sr, decay, at(c + 4), rb, lane, slice);
-            step(opb);
-            load_chain(opb, sr, decay, at(c + 5), rb, lane, slice);
-            step(opc);
-            load_chain(opc, sr, decay, at(c + 6), rb, lane, slice);
-            step(opd);
+        if constexpr (OS == 2) {
+            // three rotating operand sets (chunk c + 2 requested while chunk c is processed), so
+            // the chain fits the twelve-wave block's registers
+            ChainOps<NSUB> opa, opb, opc;
+            load_chain(opa, sr, decay, at(0), rb, lane, slice);
+            __builtin_amdgcn_sched_barrier(0);
+            load_chain(opb, sr, decay, at(1), rb, lane, slice);
+            const int NC3 = NC - NC % 3;
+            for (int c = 0; c < NC3; c += 3) {
+                load_chain(opc, sr, decay, at(c + 2), rb, lane, slice);
+                step(opa, c & 1);
+                load_chain(opa, sr, decay, at(c + 3), rb, lane, slice);
+                step(opb, (c + 1) & 1);
+                load_chain(opb, sr, decay, at(c + 4), rb, lane, slice);
+                step(opc, (c + 2) & 1);
+            }
+            if (NC3 < NC) step(opa, NC3 & 1);
+            if (NC3 + 1 < NC) step(opb, (NC3 + 1) & 1);
+        } else {
+            // four rotating operand sets: chunk c + 3 is requested while chunk c is processed
+            ChainOps<NSUB> opa, opb, opc, opd;
+            load_chain(opa, sr, decay, at(0), rb, lane, slice);
+            __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits count whole sets
+            load_chain(opb, sr, decay, at(1), rb, lane, slice);
+            __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits count whole sets
+            load_chain(opc, sr, decay, at(2), rb, lane, slice);
+            // Whole groups of four chunks, then a tail of at most three. The main loop has no
+            // early exit, so its only back edge follows the fourth step and the compiler's memory
+            // waits stay per operand set (an exit after the first step would merge into the loop
+            // header and make every group wait for the loads of the two newest sets).
+            const int NC4 = NC & ~3;
+            for (int c = 0; c < NC4; c += 4) {
+                load_chain(opd, sr, decay, at(c + 3), rb, lane, slice);
+                step(opa, 0);
+                load_chain(opa, sr, decay, at(c + 4), rb, lane, slice);
+                step(opb, 1);
+                load_chain(opb, sr, decay, at(c + 5), rb, lane, slice);
+                step(opc, 0);
+                load_chain(opc, sr, decay, at(c + 6), rb, lane, slice);
+                step(opd, 1);
+            }
+            if (NC4 < NC) step(opa, 0);
+            if (NC4 + 1 < NC) step(opb, 1);
+            if (NC4 + 2 < NC) step(opc, 0);
         }
-        if (NC4 < NC) step(opa);
-        if (NC4 + 1 < NC) step(opb);
-        if (NC4 + 2 < NC) step(opc);
         Q35_LPHASE_FLUSH();
         if (s_out) {
 #pragma unroll
@@ -1105,7 +1133,92 @@ __global__ void __launch_bounds__(ST)
                     for (int r = 0; r < 4; r++)
                         s_out[((size_t)h * DK + 32 * rb + 16 * i + 4 * grp + r) * DK + v0 + 16 * hf + col] = st[hf][i][r];
         }
+    } else if constexpr (OS == 2) {
+        // output set X = (wave - 4) / 4; its own chunks are X, X + 2, ...; own chunk k uses the
+        // operand set sp (k even) or sq (k odd), reloaded for own chunk k + 2 in the window after
+        // it is consumed
+        const int X = (uwave - 4) >> 2;
+        f32x4 acc[NSUB];
+        int pend = -1;  // the own chunk whose o waits to be stored
+        auto store_rows = [&](int r0) {
+#pragma unroll
+            for (int hf = 0; hf < NSUB; hf++)
+#pragma unroll
+                for (int r = r0; r < r0 + 2; r++) {
+                    const int t = pend * C + 16 * rb + 4 * grp + r;
+                    if (t < T) o[((size_t)t * H + h) * DK + v0 + 16 * hf + col] = to_bf16(acc[hf][r]);
+                }
+        };
+        auto own = [&](const OutOps& cur, int c) {
+            const bf16* sbt = sbt_[c & 1];
+            const bf16* vnt = vnt_[c & 1];
+            __syncthreads();  // A
+            u32x4 sb[NSUB][4];
+#pragma unroll
+            for (int hf = 0; hf < NSUB; hf++)
+#pragma unroll
+                for (int s = 0; s < 4; s++) sb[hf][s] = lds_perm(sbt + 16 * hf * SLD, SLD, col, s, grp);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int hf = 0; hf < NSUB; hf++) {
+                acc[hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 4; s++) acc[hf] = mfma16(cur.qd[s], sb[hf][s], acc[hf]);
+            }
+            __syncthreads();  // B
+            u32x4 vb[NSUB][2];
+#pragma unroll
+            for (int hf = 0; hf < NSUB; hf++) {
+                vb[hf][0] = lds_perm(vnt + 16 * hf * VLD, VLD, col, 0, grp);
+                vb[hf][1] = lds_perm(vnt + 16 * hf * VLD, VLD, col, 1, grp);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int hf = 0; hf < NSUB; hf++) {
+                acc[hf] = mfma16(cur.pb[0], vb[hf][0], acc[hf]);
+                acc[hf] = mfma16(cur.pb[1], vb[hf][1], acc[hf]);
+            }
+            pend = c;
+        };
+        // a chunk of the other set: the pending stores, half in each barrier window, and the
+        // reload of the operand set just consumed
+        auto other = [&](OutOps& reload, int c_load) {
+            __syncthreads();  // A
+            if (pend >= 0) store_rows(0);
+            load_out(reload, sr, at(c_load), rb, lane);
+            __syncthreads();  // B
+            if (pend >= 0) store_rows(2);
+        };
+        OutOps sp, sq;
+        load_out(sp, sr, at(X), rb, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        load_out(sq, sr, at(X + 2), rb, lane);
+        // groups of four chunks g .. g + 3: own chunks g + X (sp) and g + 2 + X (sq)
+        auto group = [&](int g, int lim) {
+            if (X == 0) {
+                if (0 < lim) own(sp, g);
+                if (1 < lim) other(sp, g + 4);
+                if (2 < lim) own(sq, g + 2);
+                if (3 < lim) other(sq, g + 6);
+            } else {
+                if (0 < lim) other(sq, g + 3);  // own chunk g - 1 used sq
+                if (1 < lim) own(sp, g + 1);
+                if (2 < lim) other(sp, g + 5);
+                if (3 < lim) own(sq, g + 3);
+            }
+        };
+        const int NC4 = NC & ~3;
+        for (int g = 0; g < NC4; g += 4) group(g, 4);
+        if (NC4 < NC) group(NC4, NC - NC4);
+        if (pend == NC - 1) {
+            // the last chunk was this set's, with no later window for its stores (a set's own
+            // chunk before that was stored in the windows of the chunk after it)
+            store_rows(0);
+            store_rows(2);
+        }
     } else {
+        bf16* sbt = sbt_[0];
+        bf16* vnt = vnt_[0];
         auto step = [&](const OutOps& cur, int c) {
             __syncthreads();  // A
             u32x4 sb[NSUB][4];
@@ -1233,6 +1346,16 @@ int scan_halves(int units) {
     return 146 * r2 < 100 * r1 ? 2 : 1;
 }
 
+// Output-wave sets of the one-half scan block (gdn_scan's OS). Overridable for tests by
+// Q35_SCAN_OSETS (1 or 2); both give the same bits.
+int scan_output_sets() {
+    if (const char* e = getenv("Q35_SCAN_OSETS")) {
+        const int v = atoi(e);
+        if (v == 1 || v == 2) return v;
+    }
+    return 2;
+}
+
 // One launch pair over packed sequences (gs.n > 0: T is the total row count and gs
 // describes the sequences, their chunk offsets filled here) or over one sequence (or one
 // segment of it) of T rows.
@@ -1264,8 +1387,9 @@ int gdn_launch(const void* q, const void* k, const void* v, const float* g, cons
                                                      T, H, HK, scale, gs);
     }
     const int halves = scan_halves(H * nseq);
-    auto scan = halves == 2 ? gdn_scan<2> : gdn_scan<1>;
-    scan<<<H * (DK / (BV * halves)) * nseq, ST, 0, st>>>(ws, ws.decay, static_cast<bf16*>(o), T, H, NC,
+    const int osets = halves == 1 ? scan_output_sets() : 1;
+    auto scan = halves == 2 ? gdn_scan<2, 1> : osets == 2 ? gdn_scan<1, 2> : gdn_scan<1, 1>;
+    scan<<<H * (DK / (BV * halves)) * nseq, 256 + 256 * osets, 0, st>>>(ws, ws.decay, static_cast<bf16*>(o), T, H, NC,
                                                         static_cast<const float*>(s_in), s_in_stride,
                                                         static_cast<float*>(s_out), s_out_stride, gs);
     return hipGetLastError();

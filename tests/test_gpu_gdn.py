@@ -175,6 +175,47 @@ def test_gdn_scan_block_forms_are_bit_identical(t, h, hk, varlen, monkeypatch):
     np.testing.assert_array_equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("t,h,hk,varlen", [(64, 8, 4, False), (65, 8, 4, False), (130, 6, 3, False),
+                                            (192, 16, 16, False), (300, 32, 16, False), (450, 8, 2, False),
+                                            (8229, 32, 16, False), (0, 16, 8, True)])
+def test_gdn_scan_output_sets_are_bit_identical(t, h, hk, varlen, monkeypatch):
+    """The one-half scan block runs its output with one set of four waves or with two sets
+    taking alternate chunks (bf16(S) and v_new double-buffered, the o stores in the next
+    chunk's barrier windows). Both must give the same output and final state: chunk counts
+    1 to 5 (each tail of the set and chain loops), a segmented long sequence, and packed
+    sequences including empty and one-row ones."""
+    api, st = hip.api(), stream()
+    say(f"gdn scan output sets t={t} h={h} hk={hk} varlen={varlen}")
+    monkeypatch.setenv("Q35_SCAN_HALVES", "1")
+    if not varlen:
+        q, k, v, g, b, s0 = cfg0_inputs(t, h, hk, seed=9, s0_std=0.01)
+        runs = []
+        for osets in ("1", "2"):
+            monkeypatch.setenv("Q35_SCAN_OSETS", osets)
+            runs.append(run_gdn(q, k, v, g, b, t, h, hk, s_in=s0, want_state=True))
+        np.testing.assert_array_equal(runs[0][0], runs[1][0])
+        np.testing.assert_array_equal(runs[0][1], runs[1][1])
+        return
+    lens = [64, 1, 0, 200, 129, 65, 128, 3]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    q, k, v, g, b, _ = cfg0_inputs(T, h, hk, seed=10)
+    s0 = (np.random.default_rng(11).standard_normal((len(lens), h, D, D)) * 0.01).astype(np.float32)
+    dq, dk, dv, dg, db, si = dev(q), dev(k), dev(v), dev(g), dev(b), dev(s0)
+    outs = []
+    for osets in ("1", "2"):
+        monkeypatch.setenv("Q35_SCAN_OSETS", osets)
+        o = empty(T * h * D * 2)
+        so = empty(len(lens) * h * D * D * 4)
+        ws = empty(api.cs1_gdn_workspace_floats(T + 64 * len(lens), h) * 4)
+        hip.check(api.cs1_gdn_prefill_varlen(dq.at(0), dk.at(0), dv.at(0), dg.at(0), db.at(0), o.at(0), ws.at(0),
+                                             cu.ctypes.data, len(lens), h, hk, D ** -0.5, si.at(0), h * D * D,
+                                             so.at(0), h * D * D, st.handle), "varlen")
+        outs.append((get_bf16(o, T * h * D), get(so, np.float32, len(lens) * h * D * D)))
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+
+
 @pytest.mark.parametrize("t,h,hk", [(512, 16, 16), (130, 6, 3), (107, 48, 16), (64, 8, 4)])
 def test_gdn_prep_forms_are_bit_identical(t, h, hk, monkeypatch):
     """Launches whose chunks all fit on the device at once run the 8-wave prep (gdn_prep8),
