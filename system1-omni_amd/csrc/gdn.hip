@@ -119,8 +119,7 @@ __device__ __forceinline__ float tf32_rna(float x) {
 }
 
 // 8 bf16 of a row in the permuted k order of lane group g: k = 32 s + {4g..4g+3, 16+4g..}
-__device__ __forceinline__ u32x4 load_perm(const bf16* row, int s, int g, bool valid) {
-    if (!valid) return u32x4{0u, 0u, 0u, 0u};
+__device__ __forceinline__ u32x4 load_perm(const bf16* row, int s, int g) {
     const u32x2 a = *reinterpret_cast<const u32x2*>(row + 32 * s + 4 * g);
     const u32x2 b = *reinterpret_cast<const u32x2*>(row + 32 * s + 16 + 4 * g);
     return u32x4{a[0], a[1], b[0], b[1]};
@@ -251,22 +250,30 @@ __global__ void __launch_bounds__(PT)
     //    step `wave` for all 64 tokens; gates for all tokens (lane = token). The k columns
     //    step 6 needs are the other waves' raw k rows, passed through LDS there rather than
     //    loaded a second time.
+    //    Every load is unconditional (rows past T read row T - 1) and the rows past T are zeroed
+    //    at their first use, so no load waits for another: the gates go first, and memory waits
+    //    being in issue order, the decay scan below waits only for them while the rows are in
+    //    flight.
+    const int tl = t0 + lane, tlc = min(tl, T - 1);
+    const float g_raw = g[(size_t)tlc * H + h];
+    const bf16 b_raw = beta[(size_t)tlc * H + h];
+    __builtin_amdgcn_sched_barrier(0);
     const int qb = 3 - wave;
     const int krow = 16 * wave + col, qrow = 16 * qb + col;
     u32x4 kraw[4], qraw[4], vc[4];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-        kraw[s] = load_perm(k + ((size_t)(t0 + krow) * HK + hk) * DK, s, grp, t0 + krow < T);
-        qraw[s] = load_perm(q + ((size_t)(t0 + qrow) * HK + hk) * DK, s, grp, t0 + qrow < T);
+        kraw[s] = load_perm(k + ((size_t)min(t0 + krow, T - 1) * HK + hk) * DK, s, grp);
+        qraw[s] = load_perm(q + ((size_t)min(t0 + qrow, T - 1) * HK + hk) * DK, s, grp);
     }
 #pragma unroll
     for (int tb_ = 0; tb_ < 4; tb_++) {
         const int t = t0 + 16 * tb_ + col;
-        vc[tb_] = load_perm(v + ((size_t)t * H + h) * DK, wave, grp, t < T);
+        vc[tb_] = load_perm(v + ((size_t)min(t, T - 1) * H + h) * DK, wave, grp);
     }
-    const int tl = t0 + lane;
-    const float gv = tl < T ? g[(size_t)tl * H + h] : 0.f;
-    const float bv = tl < T ? f32(beta[(size_t)tl * H + h]) : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+    const float gv = tl < T ? g_raw : 0.f;
+    const float bv = tl < T ? f32(b_raw) : 0.f;
 
     // 1. cumulative log-decay, in index order (every wave, lane = token)
     float cs = 0.f;
@@ -274,6 +281,16 @@ __global__ void __launch_bounds__(PT)
         const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
         if (j <= lane) cs = cs + gj;
     }
+    // rows past T are zero from here on
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        if (t0 + krow >= T) kraw[s] = zero4;
+        if (t0 + qrow >= T) qraw[s] = zero4;
+    }
+#pragma unroll
+    for (int tb_ = 0; tb_ < 4; tb_++)
+        if (t0 + 16 * tb_ + col >= T) vc[tb_] = zero4;
     const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs), C - 1));
     const float ec = expf(cs), er = expf(last - cs);
     if (wave == 0) {
@@ -633,29 +650,39 @@ __global__ void __launch_bounds__(PT8)
     const size_t rec = (size_t)h * NC + c;
     const int t0 = cl * C;
 
-    // 0. loads
+    // 0. loads, unconditional (rows past T read row T - 1 and are zeroed after step 1) so that
+    //    none waits for another; wave 3's gates first, which its decay scan waits for alone
     const int row = 16 * blk + col;
+    const int tl = t0 + lane;
+    float g_raw = 0.f;
+    bf16 b_raw = 0;
+    if (wave == 3) {
+        const int tlc = min(tl, T - 1);
+        g_raw = g[(size_t)tlc * H + h];
+        b_raw = beta[(size_t)tlc * H + h];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     u32x4 raw[4], vc[4];
     {
         const bf16* src = kside ? k : q;
 #pragma unroll
-        for (int s = 0; s < 4; s++) raw[s] = load_perm(src + ((size_t)(t0 + row) * HK + hk) * DK, s, grp, t0 + row < T);
+        for (int s = 0; s < 4; s++) raw[s] = load_perm(src + ((size_t)min(t0 + row, T - 1) * HK + hk) * DK, s, grp);
         if (!kside) {
 #pragma unroll
             for (int tb_ = 0; tb_ < 4; tb_++) {
                 const int t = t0 + 16 * tb_ + col;
-                vc[tb_] = load_perm(v + ((size_t)t * H + h) * DK, blk, grp, t < T);
+                vc[tb_] = load_perm(v + ((size_t)min(t, T - 1) * H + h) * DK, blk, grp);
             }
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     // 1. cumulative log-decay on wave 3 alone (lane = token), published through LDS for step
     //    3 on: one chain of 64 dependent adds in index order, lane j keeping the running sum
     //    after term j (the same additions in the same order as a per-lane prefix loop)
     if (wave == 3) {
-        const int tl = t0 + lane;
-        const float gv = tl < T ? g[(size_t)tl * H + h] : 0.f;
-        const float bv = tl < T ? f32(beta[(size_t)tl * H + h]) : 0.f;
+        const float gv = tl < T ? g_raw : 0.f;
+        const float bv = tl < T ? f32(b_raw) : 0.f;
         float run = 0.f, cs = 0.f;
 #pragma unroll
         for (int j = 0; j < C; j++) {
@@ -667,6 +694,15 @@ __global__ void __launch_bounds__(PT8)
         ecum[lane] = expf(cs);
         erem[lane] = expf(run - cs);
         if (lane == C - 1) ws.decay[rec] = expf(cs);
+    }
+    // rows past T are zero from here on
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+        if (t0 + row >= T) raw[s] = u32x4{0u, 0u, 0u, 0u};
+    if (!kside) {
+#pragma unroll
+        for (int tb_ = 0; tb_ < 4; tb_++)
+            if (t0 + 16 * tb_ + col >= T) vc[tb_] = u32x4{0u, 0u, 0u, 0u};
     }
 
     // 2. L2 norms and TF32 splits: k side -> k planes, q side -> q planes
