@@ -351,9 +351,15 @@ __global__ void __launch_bounds__(PT)
     Q35_PHASE(2);
 
     // 3. pair products. A tiles (wave, jt <= wave): rows i of this wave's k^, columns j.
+    //    The decay and beta of the lane's rows are read once, as vectors, and each tile's decay
+    //    factors are formed for every element and masked by a select: per-element reads inside
+    //    the j <= i branches each waited for the LDS.
+    const f32x4 cum_i = *reinterpret_cast<const f32x4*>(cum + 16 * wave + 4 * grp);
+    const f32x4 bet_i = *reinterpret_cast<const f32x4*>(bet + 16 * wave + 4 * grp);
 #pragma unroll
     for (int jt = 0; jt < 4; jt++) {
         if (jt > wave) continue;
+        const float cum_j = cum[16 * jt + col];
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; s++) {
@@ -364,21 +370,25 @@ __global__ void __launch_bounds__(PT)
             acc = mfma16(khi[s], bh, acc);
         }
         const int j = 16 * jt + col;
+        float dec[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) dec[r] = expf(cum_i[r] - cum_j);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int i = 16 * wave + 4 * grp + r;
-            const float dec = j <= i ? expf(cum[i] - cum[j]) : 0.f;
-            am[i * FLD + j] = j < i ? bet[i] * acc[r] * dec : 0.f;
+            am[i * FLD + j] = j < i ? bet_i[r] * acc[r] * dec[r] : 0.f;
         }
     }
     // P^T tiles (jt <= qb, qb): rows j of k^ (planes), columns i of this wave's q^ rows.
     // pb fragment (qb, s) = tiles 2s and 2s + 1, lane for lane.
     {
         f32x4 pt[4];
+        const float cum_q = cum[qrow];
 #pragma unroll
         for (int jt = 0; jt < 4; jt++) {
             pt[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
             if (jt > qb) continue;
+            const f32x4 cum_j = *reinterpret_cast<const f32x4*>(cum + 16 * jt + 4 * grp);
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 const u32x4 ah = khi_pl[(jt * 4 + s) * FRAG + lane], al = klo_pl[(jt * 4 + s) * FRAG + lane];
@@ -388,10 +398,13 @@ __global__ void __launch_bounds__(PT)
                 pt[jt] = mfma16(ah, qhi[s], pt[jt]);
             }
             const int i = qrow;
+            float dec[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) dec[r] = expf(cum_q - cum_j[r]);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int j = 16 * jt + 4 * grp + r;
-                pt[jt][r] = j <= i ? round_bf16(pt[jt][r] * expf(cum[i] - cum[j])) : 0.f;
+                pt[jt][r] = j <= i ? round_bf16(pt[jt][r] * dec[r]) : 0.f;
             }
         }
         ws.pb[(rec * 8 + qb * 2 + 0) * FRAG + lane] = pack_pair(pt[0], pt[1]);
@@ -561,6 +574,10 @@ __device__ __forceinline__ void store_through(V* frag, int lane, V v) {
 __device__ __forceinline__ void prep8_a_tile(int bi, int bj, const u32x4* khi_pl, const u32x4* klo_pl, float* am,
                                              const float* cum, const float* bet, int lane) {
     const int col = lane & 15, grp = lane >> 4;
+    // decay and beta as vectors up front, decay factors masked by a select (see gdn_prep)
+    const f32x4 cum_i = *reinterpret_cast<const f32x4*>(cum + 16 * bi + 4 * grp);
+    const f32x4 bet_i = *reinterpret_cast<const f32x4*>(bet + 16 * bi + 4 * grp);
+    const float cum_j = cum[16 * bj + col];
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; s++) {
@@ -572,11 +589,13 @@ __device__ __forceinline__ void prep8_a_tile(int bi, int bj, const u32x4* khi_pl
         acc = mfma16(ah, bh, acc);
     }
     const int j = 16 * bj + col;
+    float dec[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) dec[r] = expf(cum_i[r] - cum_j);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int i = 16 * bi + 4 * grp + r;
-        const float dec = j <= i ? expf(cum[i] - cum[j]) : 0.f;
-        am[i * FLD + j] = j < i ? bet[i] * acc[r] * dec : 0.f;
+        am[i * FLD + j] = j < i ? bet_i[r] * acc[r] * dec[r] : 0.f;
     }
 }
 
@@ -586,11 +605,13 @@ __device__ __forceinline__ void prep8_p_frag(int qb, int s2, const u32x4* khi_pl
                                              const Work& ws, size_t rec, int lane) {
     const int col = lane & 15, grp = lane >> 4;
     f32x4 pt[2];
+    const float cum_q = cum[16 * qb + col];
 #pragma unroll
     for (int p = 0; p < 2; p++) {
         const int jt = 2 * s2 + p;
         pt[p] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (jt > qb) continue;
+        const f32x4 cum_j = *reinterpret_cast<const f32x4*>(cum + 16 * jt + 4 * grp);
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             const u32x4 ah = khi_pl[(jt * 4 + s) * FRAG + lane], al = klo_pl[(jt * 4 + s) * FRAG + lane];
@@ -601,10 +622,13 @@ __device__ __forceinline__ void prep8_p_frag(int qb, int s2, const u32x4* khi_pl
             pt[p] = mfma16(ah, qh, pt[p]);
         }
         const int i = 16 * qb + col;
+        float dec[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) dec[r] = expf(cum_q - cum_j[r]);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int j = 16 * jt + 4 * grp + r;
-            pt[p][r] = j <= i ? round_bf16(pt[p][r] * expf(cum[i] - cum[j])) : 0.f;
+            pt[p][r] = j <= i ? round_bf16(pt[p][r] * dec[r]) : 0.f;
         }
     }
     store_through(&ws.pb[(rec * 8 + qb * 2 + s2) * FRAG], lane, pack_pair(pt[0], pt[1]));
