@@ -208,6 +208,38 @@ __device__ unsigned long long q35_phase_ticks[16];
 #define Q35_LPHASE_FLUSH() (void)0
 #endif
 
+// Off-diagonal level LV of the blocked inverse for the wave owning row block bi >= LV:
+// T_{bi, bi - LV} = -T_ii (sum_k A_ik T_kj), k over the LV blocks bi - LV .. bi - 1, on the f32
+// MFMA (A operand: lane = row l%16, k = l/16; B operand: lane = column l%16, k = l/16). The
+// level's trip counts are constants, so every operand is read from LDS ahead of the MFMA chain
+// (the products and their order are those of a loop over the blocks). The partial product
+// passes through the wave's own scratch, whose writes precede its reads in the wave's LDS order.
+template <int LV>
+__device__ __forceinline__ void inverse_level(int bi, const float* am, float* tm, float* scr, int col, int grp) {
+    const int bj = bi - LV;
+    float a[4 * LV], t[4 * LV], tii[4];
+#pragma unroll
+    for (int m = 0; m < LV; m++)
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const int kb = bj + m;
+            a[4 * m + kk] = am[(16 * bi + col) * FLD + 16 * kb + 4 * kk + grp];
+            t[4 * m + kk] = tm[(16 * kb + 4 * kk + grp) * FLD + 16 * bj + col];
+        }
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) tii[kk] = tm[(16 * bi + col) * FLD + 16 * bi + 4 * kk + grp];
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int x = 0; x < 4 * LV; x++) acc = mfma_f32(a[x], t[x], acc);
+#pragma unroll
+    for (int r = 0; r < 4; r++) scr[(4 * grp + r) * 16 + col] = acc[r];
+    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) acc = mfma_f32(tii[kk], scr[(4 * kk + grp) * 16 + col], acc);
+#pragma unroll
+    for (int r = 0; r < 4; r++) tm[(16 * bi + 4 * grp + r) * FLD + 16 * bj + col] = -acc[r];
+}
+
 __global__ void __launch_bounds__(PT)
     gdn_prep(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
              const float* __restrict__ g, const bf16* __restrict__ beta, Work ws, int T, int H, int HK, float scale,
@@ -436,32 +468,13 @@ __global__ void __launch_bounds__(PT)
     }
     __syncthreads();
     Q35_PHASE(4);
-    //    levels: wave bi computes T_{bi, bi - lv} = -T_ii (sum_k A_ik T_kj) on the f32 MFMA
-    //    (A operand: lane = row l%16, k = l/16; B operand: lane = column l%16, k = l/16)
-    for (int lv = 1; lv < 4; lv++) {
-        const int bi = wave, bj = wave - lv;
-        const bool active = bj >= 0;
-        if (active) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            for (int kb = bj; kb < bi; kb++)
-#pragma unroll
-                for (int kk = 0; kk < 4; kk++)
-                    acc = mfma_f32(am[(16 * bi + col) * FLD + 16 * kb + 4 * kk + grp],
-                                   tm[(16 * kb + 4 * kk + grp) * FLD + 16 * bj + col], acc);
-#pragma unroll
-            for (int r = 0; r < 4; r++) scr[(4 * grp + r) * 16 + col] = acc[r];
-        }
-        // scr is this wave's own: its writes precede its reads in the wave's LDS order
-        if (active) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-                acc = mfma_f32(tm[(16 * bi + col) * FLD + 16 * bi + 4 * kk + grp], scr[(4 * kk + grp) * 16 + col], acc);
-#pragma unroll
-            for (int r = 0; r < 4; r++) tm[(16 * bi + 4 * grp + r) * FLD + 16 * bj + col] = -acc[r];
-        }
-        __syncthreads();
-    }
+    //    the off-diagonal levels, wave bi computing T_{bi, bi - lv}
+    if (wave >= 1) inverse_level<1>(wave, am, tm, scr, col, grp);
+    __syncthreads();
+    if (wave >= 2) inverse_level<2>(wave, am, tm, scr, col, grp);
+    __syncthreads();
+    if (wave >= 3) inverse_level<3>(wave, am, tm, scr, col, grp);
+    __syncthreads();
     Q35_PHASE(5);
 
     // 5. Tb = bf16(T beta_j); the raw k rows go to region 1 (A is dead) for step 6
@@ -896,30 +909,12 @@ __global__ void __launch_bounds__(PT8)
     __syncthreads();
     if (!kside) transposes();
     float* scr = reinterpret_cast<float*>(sm + R0_SC) + blk * 256;
-    for (int lv = 1; lv < 4; lv++) {
-        const int bi = blk, bj = blk - lv;
-        const bool active = kside && bj >= 0;
-        if (active) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            for (int kb = bj; kb < bi; kb++)
-#pragma unroll
-                for (int kk = 0; kk < 4; kk++)
-                    acc = mfma_f32(am[(16 * bi + col) * FLD + 16 * kb + 4 * kk + grp],
-                                   tm[(16 * kb + 4 * kk + grp) * FLD + 16 * bj + col], acc);
-#pragma unroll
-            for (int r = 0; r < 4; r++) scr[(4 * grp + r) * 16 + col] = acc[r];
-        }
-        // scr is this wave's own: its writes precede its reads in the wave's LDS order
-        if (active) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-                acc = mfma_f32(tm[(16 * bi + col) * FLD + 16 * bi + 4 * kk + grp], scr[(4 * kk + grp) * 16 + col], acc);
-#pragma unroll
-            for (int r = 0; r < 4; r++) tm[(16 * bi + 4 * grp + r) * FLD + 16 * bj + col] = -acc[r];
-        }
-        __syncthreads();
-    }
+    if (kside && blk >= 1) inverse_level<1>(blk, am, tm, scr, col, grp);
+    __syncthreads();
+    if (kside && blk >= 2) inverse_level<2>(blk, am, tm, scr, col, grp);
+    __syncthreads();
+    if (kside && blk >= 3) inverse_level<3>(blk, am, tm, scr, col, grp);
+    __syncthreads();
 
     // 5. Tb = bf16(T beta_j)
     for (int x = tid; x < C * C; x += PT8) {
