@@ -111,11 +111,23 @@ Work split(float* workspace, size_t NC, int H) {
                 reinterpret_cast<u32x2*>(b + l.u),  reinterpret_cast<float*>(b + l.decay)};
 }
 
-// cvt.rna.tf32.f32: 10 explicit mantissa bits, round half away from zero.
+// cvt.rna.tf32.f32 for finite x: 10 explicit mantissa bits, round half away from zero (the
+// operands here are L2-normalised rows, always finite).
 __device__ __forceinline__ float tf32_rna(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7f800000u) != 0x7f800000u) u = (u + 0x1000u) & 0xffffe000u;
-    return __uint_as_float(u);
+    return __uint_as_float((__float_as_uint(x) + 0x1000u) & 0xffffe000u);
+}
+
+// The exact two-term bf16 split of eight TF32-rounded values: hi = rne_bf16(t) (a TF32 value
+// has 11 significant bits, so lo = t - hi is exact in bf16), both packed in operand order. The
+// packed hi comes straight from the pairwise conversion and is unpacked once for the
+// subtraction.
+__device__ __forceinline__ void split_tf32(const float t[8], u32x4& hi, u32x4& lo) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t h = pack2(t[2 * i], t[2 * i + 1]);
+        hi[i] = h;
+        lo[i] = pack2(t[2 * i] - lo_f32(h), t[2 * i + 1] - hi_f32(h));
+    }
 }
 
 // 8 bf16 of a row in the permuted k order of lane group g: k = 32 s + {4g..4g+3, 16+4g..}
@@ -357,24 +369,18 @@ __global__ void __launch_bounds__(PT)
     u32x4 khi[4], klo[4], qhi[4], qlo[4];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-        float hk_[8], lk_[8], hq_[8], lq_[8], qd_[8], kf[8], qf[8];
+        float kt_[8], qt_[8], qd_[8], kf[8], qf[8];
         unpack8v(kraw[s], kf);
         unpack8v(qraw[s], qf);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const float kt = tf32_rna(kf[e] * kinv);
-            hk_[e] = round_bf16(kt);
-            lk_[e] = kt - hk_[e];
+            kt_[e] = tf32_rna(kf[e] * kinv);
             const float qx = qf[e] * qinv;
-            const float qt = tf32_rna(qx);
-            hq_[e] = round_bf16(qt);
-            lq_[e] = qt - hq_[e];
+            qt_[e] = tf32_rna(qx);
             qd_[e] = qx * ecq;
         }
-        khi[s] = pack8v(hk_);
-        klo[s] = pack8v(lk_);
-        qhi[s] = pack8v(hq_);
-        qlo[s] = pack8v(lq_);
+        split_tf32(kt_, khi[s], klo[s]);
+        split_tf32(qt_, qhi[s], qlo[s]);
         khi_pl[(wave * 4 + s) * FRAG + lane] = khi[s];
         klo_pl[(wave * 4 + s) * FRAG + lane] = klo[s];
         ws.qd[(rec * 16 + qb * 4 + s) * FRAG + lane] = pack8v(qd_);
@@ -760,31 +766,27 @@ __global__ void __launch_bounds__(PT8)
             if (grp == 0) kinv_s[row] = kinv;
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                float hk_[8], lk_[8], kf[8];
+                float kt_[8], kf[8];
                 unpack8v(raw[s], kf);
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float kt = tf32_rna(kf[e] * kinv);
-                    hk_[e] = round_bf16(kt);
-                    lk_[e] = kt - hk_[e];
-                }
-                khi_pl[(blk * 4 + s) * FRAG + lane] = pack8v(hk_);
-                klo_pl[(blk * 4 + s) * FRAG + lane] = pack8v(lk_);
+                for (int e = 0; e < 8; e++) kt_[e] = tf32_rna(kf[e] * kinv);
+                u32x4 h, l;
+                split_tf32(kt_, h, l);
+                khi_pl[(blk * 4 + s) * FRAG + lane] = h;
+                klo_pl[(blk * 4 + s) * FRAG + lane] = l;
             }
         } else {
             qinv = rsqrtf(ss + 1e-6f) * scale;
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                float hq_[8], lq_[8], qf[8];
+                float qt_[8], qf[8];
                 unpack8v(raw[s], qf);
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float qt = tf32_rna(qf[e] * qinv);
-                    hq_[e] = round_bf16(qt);
-                    lq_[e] = qt - hq_[e];
-                }
-                qhi_pl[(blk * 4 + s) * FRAG + lane] = pack8v(hq_);
-                qlo_pl[(blk * 4 + s) * FRAG + lane] = pack8v(lq_);
+                for (int e = 0; e < 8; e++) qt_[e] = tf32_rna(qf[e] * qinv);
+                u32x4 h, l;
+                split_tf32(qt_, h, l);
+                qhi_pl[(blk * 4 + s) * FRAG + lane] = h;
+                qlo_pl[(blk * 4 + s) * FRAG + lane] = l;
             }
         }
     }
