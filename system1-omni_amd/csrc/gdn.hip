@@ -446,7 +446,9 @@ __global__ void __launch_bounds__(PT)
             }
         }
         ws.pb[(rec * 8 + qb * 2 + 0) * FRAG + lane] = pack_pair(pt[0], pt[1]);
-        ws.pb[(rec * 8 + qb * 2 + 1) * FRAG + lane] = pack_pair(pt[2], pt[3]);
+        // fragment (qb, 1) of row blocks 0 and 1 lies above the diagonal: all zero, neither
+        // written nor read
+        if (qb >= 2) ws.pb[(rec * 8 + qb * 2 + 1) * FRAG + lane] = pack_pair(pt[2], pt[3]);
     }
     __syncthreads();
     Q35_PHASE(3);
@@ -804,8 +806,8 @@ __global__ void __launch_bounds__(PT8)
         }
     }
 
-    // 3. pair products by table: 10 A tiles and the 8 pb fragments (two of them all zero: the
-    //    scan reads every fragment) over 8 waves
+    // 3. pair products by table: 10 A tiles and the 6 pb fragments that are not all zero (the
+    //    scan never reads fragment 1 of row blocks 0 and 1) over 8 waves
     switch (wave) {
         case 0:
             prep8_a_tile(3, 3, khi_pl, klo_pl, am, cum, bet, lane);
@@ -828,11 +830,9 @@ __global__ void __launch_bounds__(PT8)
             break;
         case 4:
             prep8_p_frag(3, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
-            prep8_p_frag(0, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);  // zeros
             break;
         case 5:
             prep8_p_frag(3, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
-            prep8_p_frag(1, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);  // zeros
             break;
         case 6:
             prep8_p_frag(2, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
@@ -1006,8 +1006,9 @@ __device__ __forceinline__ void load_out(OutOps& op, const Streams& sr, int c, i
     const int v16 = lane * 16;
 #pragma unroll
     for (int s = 0; s < 4; s++) op.qd[s] = bload16(sr.qd, v16 + s * 1024, c * 16 * 1024 + rb * 4 * 1024);
-#pragma unroll
-    for (int s = 0; s < 2; s++) op.pb[s] = bload16(sr.pb, v16 + s * 1024, c * 8 * 1024 + rb * 2 * 1024);
+    op.pb[0] = bload16(sr.pb, v16, c * 8 * 1024 + rb * 2 * 1024);
+    // token step 1 of row blocks 0 and 1 lies above the diagonal (all zero, not stored)
+    if (rb >= 2) op.pb[1] = bload16(sr.pb, v16 + 1024, c * 8 * 1024 + rb * 2 * 1024);
 }
 
 // B operand from a [16][ld] bf16 LDS array: row `col`, k step s in perm order
@@ -1233,7 +1234,7 @@ __global__ void __launch_bounds__(256 + 256 * OS)
 #pragma unroll
             for (int hf = 0; hf < NSUB; hf++) {
                 acc[hf] = mfma16(cur.pb[0], vb[hf][0], acc[hf]);
-                acc[hf] = mfma16(cur.pb[1], vb[hf][1], acc[hf]);
+                if (rb >= 2) acc[hf] = mfma16(cur.pb[1], vb[hf][1], acc[hf]);
             }
             pend = c;
         };
@@ -1302,7 +1303,7 @@ __global__ void __launch_bounds__(256 + 256 * OS)
 #pragma unroll
             for (int hf = 0; hf < NSUB; hf++) {
                 acc[hf] = mfma16(cur.pb[0], vb[hf][0], acc[hf]);
-                acc[hf] = mfma16(cur.pb[1], vb[hf][1], acc[hf]);
+                if (rb >= 2) acc[hf] = mfma16(cur.pb[1], vb[hf][1], acc[hf]);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int t = c * C + 16 * rb + 4 * grp + r;
