@@ -696,7 +696,10 @@ def main():
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) inputs of the benchmark shapes)",
         "config": {"workload": attn["workload"], "global_batch": 1, "seq_len": 2048, "parallelism": "none"},
         "roofline": {k: attn["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac")} |
-                    {"traffic": traffic_bytes("q35::(anonymous namespace)::flash32_kernel<true, false> grid=131072 ")},
+                    {"traffic": traffic_bytes("q35::(anonymous namespace)::flash32_kernel<true, false> grid=131072 "),
+                     # HBM bytes per launch are not counted in this run: they come from the committed
+                     # FETCH_SIZE / WRITE_SIZE counter passes over `bench.py --probe`
+                     "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT)},
         "cpu_baseline": cpu,
         "layers": {"attention_cfg1": attn, "attention_t8192": attn8k, "attention_cfg3_dh256": attn256,
                    "gdn_cfg2": g2, "gdn_cfg0": g0},
