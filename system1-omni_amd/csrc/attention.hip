@@ -1078,12 +1078,9 @@ __global__ void __launch_bounds__(512, 1)
         const unsigned char* kb = smem + sc * STAGE;
         const unsigned char* vb = smem + (sc == 0 ? 2 : sc - 1) * STAGE + K_BYTES;
         const int xr = ((it + 1) & 1) * XCH, xw = (it & 1) * XCH;
-        u32x4 kfr[8], vfr[2][2];
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++)
-            kfr[ks] = *reinterpret_cast<const u32x4*>(kb + kf + (k_slot(c32, 16 * dh + 2 * ks + hh) << 4));
+        u32x4 kfr[8], vfr[4][2];
         // the partner's partial scores of tile it - 1 (step 0: of the empty tile, whose scores
-        // are masked below)
+        // are masked below), read ahead of the K fragments so the softmax does not wait for them
         f32x16 s;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -1091,6 +1088,9 @@ __global__ void __launch_bounds__(512, 1)
 #pragma unroll
             for (int e = 0; e < 4; e++) s[4 * j + e] = x[e];
         }
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            kfr[ks] = *reinterpret_cast<const u32x4*>(kb + kf + (k_slot(c32, 16 * dh + 2 * ks + hh) << 4));
         __builtin_amdgcn_sched_barrier(0);
         dma_k(it + 2, sc == 0 ? 2 : sc - 1, it + 2 < ntiles);
         __builtin_amdgcn_sched_barrier(0);
@@ -1143,17 +1143,20 @@ __global__ void __launch_bounds__(512, 1)
         __builtin_amdgcn_sched_barrier(0);
         dma_v(it + 1, sc == 2 ? 0 : sc + 1, it + 1 < ntiles);
         __builtin_amdgcn_sched_barrier(0);
-        // P V for this wave's 128 dims, V^T fragments read per dim tile
+        // P V for this wave's 128 dims: every V^T fragment is read before the first MFMA, so
+        // the reads of later dim tiles overlap the MFMAs of earlier ones
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const u32x2 lo = read_tr(vb + vt(t, j, 0)), hi = read_tr(vb + vt(t, j, 1));
-                vfr[t & 1][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+                vfr[t][j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
             }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < 2; j++) o[t] = mfma32(vfr[t & 1][j], pf[j], o[t]);
-        }
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) o[t] = mfma32(vfr[t][j], pf[j], o[t]);
         __builtin_amdgcn_s_waitcnt(VMCNT_ONE_STEP);
         __syncthreads();
     };
