@@ -200,6 +200,15 @@ __device__ unsigned long long q35_phase_ticks[16];
         if (threadIdx.x == 0) atomicAdd(&q35_phase_ticks[i], q35_t1 - q35_t0);   \
         q35_t0 = q35_t1;                                                         \
     } while (0)
+// per wave of gdn_prep8: clocks from the block's start to point i, summed over blocks
+__device__ unsigned long long q35_wave_ticks[64];
+#define Q35_WSTART() uint64_t q35_w0 = __builtin_amdgcn_s_memtime(), q35_ws[8] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define Q35_WSTAMP(i) q35_ws[i] = __builtin_amdgcn_s_memtime() - q35_w0
+#define Q35_WFLUSH()                                                                             \
+    do {                                                                                         \
+        if ((threadIdx.x & 63) == 0)                                                             \
+            for (int q35_i = 0; q35_i < 8; q35_i++) atomicAdd(&q35_wave_ticks[(threadIdx.x >> 6) * 8 + q35_i], q35_ws[q35_i]); \
+    } while (0)
 #define Q35_LPHASE_START() uint64_t q35_t0 = __builtin_amdgcn_s_memtime(), q35_acc[5] = {0, 0, 0, 0, 0}
 #define Q35_LPHASE(i)                                          \
     do {                                                       \
@@ -214,6 +223,9 @@ __device__ unsigned long long q35_phase_ticks[16];
     } while (0)
 #else
 #define Q35_PHASE_START() (void)0
+#define Q35_WSTART() (void)0
+#define Q35_WSTAMP(i) (void)0
+#define Q35_WFLUSH() (void)0
 #define Q35_PHASE(i) (void)0
 #define Q35_LPHASE_START() (void)0
 #define Q35_LPHASE(i) (void)0
@@ -574,7 +586,43 @@ __global__ void __launch_bounds__(PT)
 // values as in gdn_prep, so the records are bit for bit the same.
 constexpr int PT8 = 512;
 constexpr int QPL = PREP_SMEM;                         // q^ planes: hi then lo, [4 blocks][4 steps]
-constexpr int PREP8_SMEM = QPL + 2 * PLANE;
+// input rows staged by LDS DMA: k, q and v of the chunk, [64 rows][256 B] each
+constexpr int STG_ROW = DK * 2;
+constexpr int STG_K = QPL + 2 * PLANE;
+constexpr int STG_Q = STG_K + C * STG_ROW;
+constexpr int STG_V = STG_Q + C * STG_ROW;
+constexpr int PREP8_SMEM = STG_V + C * STG_ROW;
+static_assert(PREP8_SMEM <= 160 * 1024, "gdn_prep8 fits the LDS");
+
+// A buffer load of 16 bytes per lane straight into LDS: lane l's chunk lands at lds + 16 l.
+// (A __device__ function: the builtin used inside a kernel's lambda kept the host pass from
+// emitting the kernel's launch stub.)
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, int voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+// Rows rl0 .. rl0 + 15 of a chunk (token t0 + rl at base + t ld, 256 bytes; rows past T read
+// row T - 1) into the staging area stg as whole cache lines: 16-byte chunk c of row rl sits at
+// chunk position c ^ (rl % 16), so the permuted reads of staged_perm hit distinct banks.
+__device__ __forceinline__ void stage_rows(const bf16* base, int ld, int t0, int rl0, int T, unsigned char* stg,
+                                           int lane) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(base), (short)0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int rl = rl0 + 4 * i + (lane >> 4);
+        const int c = (lane & 15) ^ (rl & 15);
+        const int t = min(t0 + rl, T - 1);
+        lds_load16(rs, stg + (rl0 + 4 * i) * STG_ROW, t * ld * 2 + 16 * c);
+    }
+}
+
+// load_perm's 8 values of staged row rl: dims 32 s + 4 g .. + 3 and 32 s + 16 + 4 g .. + 3
+__device__ __forceinline__ u32x4 staged_perm(const unsigned char* stg, int rl, int s, int g) {
+    const unsigned char* rp = stg + rl * STG_ROW + 8 * (g & 1);
+    const u32x2 a = *reinterpret_cast<const u32x2*>(rp + (((4 * s + (g >> 1)) ^ (rl & 15)) << 4));
+    const u32x2 b = *reinterpret_cast<const u32x2*>(rp + (((4 * s + 2 + (g >> 1)) ^ (rl & 15)) << 4));
+    return u32x4{a[0], a[1], b[0], b[1]};
+}
 
 // One fragment (64 lanes x 16 or 8 bytes at frag, a wave-uniform address) stored at device
 // scope (the SC1 cache-policy bit): the line is written through the XCD's L2 instead of being
@@ -694,40 +742,38 @@ __global__ void __launch_bounds__(PT8)
     const int blk = wave & 3;  // k row block (k side) / q row block and v dim step (q side)
     const size_t rec = (size_t)h * NC + c;
     const int t0 = cl * C;
+    Q35_PHASE_START();
+    Q35_WSTART();
 
     // 0. loads, unconditional (rows past T read row T - 1 and are zeroed after step 1) so that
-    //    none waits for another; wave 3's gates first, which its decay scan waits for alone
+    //    none waits for another; wave 3's gates first, which its decay scan waits for alone.
+    //    The k and q rows go to LDS as whole lines (a fragment's pieces are half lines 4 KB
+    //    apart) and are read back in fragment order.
     const int row = 16 * blk + col;
     const int tl = t0 + lane;
+    // (the gate loads are issued by hand and waited for by hand, together with the four row
+    // transfers issued after them: as ordinary loads the compiler placed the wait for beta, or
+    // the loads themselves, after the transfers were issued or before them)
     float g_raw = 0.f;
-    bf16 b_raw = 0;
+    uint32_t b_bits = 0;
     if (wave == 3) {
         const int tlc = min(tl, T - 1);
-        g_raw = g[(size_t)tlc * H + h];
-        b_raw = beta[(size_t)tlc * H + h];
+        asm volatile("global_load_dword %0, %1, off" : "=v"(g_raw) : "v"(g + (size_t)tlc * H + h));
+        asm volatile("global_load_ushort %0, %1, off" : "=v"(b_bits) : "v"(beta + (size_t)tlc * H + h));
     }
     __builtin_amdgcn_sched_barrier(0);
-    u32x4 raw[4], vc[4];
-    {
-        const bf16* src = kside ? k : q;
-#pragma unroll
-        for (int s = 0; s < 4; s++) raw[s] = load_perm(src + ((size_t)min(t0 + row, T - 1) * HK + hk) * DK, s, grp);
-        if (!kside) {
-#pragma unroll
-            for (int tb_ = 0; tb_ < 4; tb_++) {
-                const int t = t0 + 16 * tb_ + col;
-                vc[tb_] = load_perm(v + ((size_t)min(t, T - 1) * H + h) * DK, blk, grp);
-            }
-        }
-    }
+    unsigned char* const stg = sm + (kside ? STG_K : STG_Q);
+    stage_rows((kside ? k : q) + (size_t)hk * DK, HK * DK, t0, 16 * blk, T, stg, lane);
     __builtin_amdgcn_sched_barrier(0);
 
     // 1. cumulative log-decay on wave 3 alone (lane = token), published through LDS for step
     //    3 on: one chain of 64 dependent adds in index order, lane j keeping the running sum
     //    after term j (the same additions in the same order as a per-lane prefix loop)
+    Q35_WSTAMP(0);
     if (wave == 3) {
+        asm volatile("s_waitcnt vmcnt(4)" : "+v"(g_raw), "+v"(b_bits));
         const float gv = tl < T ? g_raw : 0.f;
-        const float bv = tl < T ? f32(b_raw) : 0.f;
+        const float bv = tl < T ? __uint_as_float(b_bits << 16) : 0.f;
         float run = 0.f, cs = 0.f;
 #pragma unroll
         for (int j = 0; j < C; j++) {
@@ -738,17 +784,21 @@ __global__ void __launch_bounds__(PT8)
         bet[lane] = bv;
         ecum[lane] = expf(cs);
         erem[lane] = expf(run - cs);
-        if (lane == C - 1) ws.decay[rec] = expf(cs);
     }
-    // rows past T are zero from here on
+#ifdef Q35_PHASE_TIMING
+    if (wave == 3) asm volatile("" ::"v"(ecum[lane]));
+#endif
+    Q35_WSTAMP(1);
+    // the wave's own rows from LDS; then the q side stages the v rows, read by dim step after
+    // the next barrier. Rows past T are zero from here on.
+    wait_vm_all();
+    u32x4 raw[4], vc[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) raw[s] = staged_perm(stg, row, s, grp);
+    if (!kside) stage_rows(v + (size_t)h * DK, H * DK, t0, 16 * blk, T, sm + STG_V, lane);
 #pragma unroll
     for (int s = 0; s < 4; s++)
         if (t0 + row >= T) raw[s] = u32x4{0u, 0u, 0u, 0u};
-    if (!kside) {
-#pragma unroll
-        for (int tb_ = 0; tb_ < 4; tb_++)
-            if (t0 + 16 * tb_ + col >= T) vc[tb_] = u32x4{0u, 0u, 0u, 0u};
-    }
 
     // 2. L2 norms and TF32 splits: k side -> k planes, q side -> q planes
     float qinv = 0.f;
@@ -761,6 +811,8 @@ __global__ void __launch_bounds__(PT8)
 #pragma unroll
             for (int e = 0; e < 8; e++) ss += xf[e] * xf[e];
         }
+        asm volatile("" ::"v"(ss));
+        Q35_WSTAMP(2);
         ss += __shfl_xor(ss, 16, 64);
         ss += __shfl_xor(ss, 32, 64);
         if (kside) {
@@ -792,9 +844,18 @@ __global__ void __launch_bounds__(PT8)
             }
         }
     }
+    Q35_WSTAMP(3);
+    if (!kside) wait_vm_all();  // the staged v rows
     __syncthreads();
+    Q35_PHASE(2);
+    Q35_WSTAMP(4);
     // qd = (q^ scale) e^cum once the cumulative decay is in LDS
     if (!kside) {
+#pragma unroll
+        for (int tb_ = 0; tb_ < 4; tb_++) {
+            vc[tb_] = staged_perm(sm + STG_V, 16 * tb_ + col, blk, grp);
+            if (t0 + 16 * tb_ + col >= T) vc[tb_] = u32x4{0u, 0u, 0u, 0u};
+        }
         const float ecq = ecum[row];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
@@ -842,7 +903,9 @@ __global__ void __launch_bounds__(PT8)
             prep8_p_frag(1, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
             break;
     }
+    Q35_WSTAMP(5);
     __syncthreads();
+    Q35_PHASE(3);
 
     // 4. T = (I + A)^-1: zero upper blocks (all threads), diagonal blocks on waves 0-3. The raw
     //    k rows go to the q-plane region (dead after step 3) for step 6's transposes, which the
@@ -909,6 +972,7 @@ __global__ void __launch_bounds__(PT8)
         for (int r = 0; r < 16; r++) tm[(base + r) * FLD + base + cc] = xs[r];
     }
     __syncthreads();
+    Q35_PHASE(4);
     if (!kside) transposes();
     float* scr = reinterpret_cast<float*>(sm + R0_SC) + blk * 256;
     if (kside && blk >= 1) inverse_level<1>(blk, am, tm, scr, col, grp);
@@ -917,6 +981,7 @@ __global__ void __launch_bounds__(PT8)
     __syncthreads();
     if (kside && blk >= 3) inverse_level<3>(blk, am, tm, scr, col, grp);
     __syncthreads();
+    Q35_PHASE(5);
 
     // 5. Tb = bf16(T beta_j)
     for (int x = tid; x < C * C; x += PT8) {
@@ -924,6 +989,7 @@ __global__ void __launch_bounds__(PT8)
         tb[i * TLD + j] = to_bf16(tm[i * FLD + j] * bet[j]);
     }
     __syncthreads();
+    Q35_PHASE(6);
 
     // 6. u = Tb v on the q side (its transposes ran in step 4); on the k side the kw transpose
     //    and w^T = kw^T Tb^T
@@ -949,6 +1015,11 @@ __global__ void __launch_bounds__(PT8)
         }
         if (kside) store_through(&ws.w[(rec * 16 + it * 4 + ds) * FRAG], lane, pack_pair(wt[0], wt[1]));
     }
+    // the chunk's decay, stored last: a store before a block barrier is waited for there
+    if (wave == 3 && lane == C - 1) ws.decay[rec] = ecum[C - 1];
+    Q35_PHASE(7);
+    Q35_WSTAMP(6);
+    Q35_WFLUSH();
 }
 
 // ------------------------------------------------------------------ gdn_scan
@@ -1504,6 +1575,9 @@ using namespace q35;
 #ifdef Q35_PHASE_TIMING
 extern "C" int q35_debug_phase_ticks(unsigned long long* out) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(q35_phase_ticks), sizeof(q35_phase_ticks));
+}
+extern "C" int q35_debug_wave_ticks(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(q35_wave_ticks), sizeof(q35_wave_ticks));
 }
 #endif
 
