@@ -264,6 +264,38 @@ __device__ __forceinline__ void inverse_level(int bi, const float* am, float* tm
     for (int r = 0; r < 4; r++) tm[(16 * bi + 4 * grp + r) * FLD + 16 * bj + col] = -acc[r];
 }
 
+constexpr int STG_ROW = DK * 2;  // bytes of a staged input row
+
+// A buffer load of 16 bytes per lane straight into LDS: lane l's chunk lands at lds + 16 l.
+// (A __device__ function: the builtin used inside a kernel's lambda kept the host pass from
+// emitting the kernel's launch stub.)
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, int voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+// Rows rl0 .. rl0 + 15 of a chunk (token t0 + rl at base + t ld, 256 bytes; rows past T read
+// row T - 1) into the staging area stg as whole cache lines: 16-byte chunk c of row rl sits at
+// chunk position c ^ (rl % 16), so the permuted reads of staged_perm hit distinct banks.
+__device__ __forceinline__ void stage_rows(const bf16* base, int ld, int t0, int rl0, int T, unsigned char* stg,
+                                           int lane) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(base), (short)0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int rl = rl0 + 4 * i + (lane >> 4);
+        const int c = (lane & 15) ^ (rl & 15);
+        const int t = min(t0 + rl, T - 1);
+        lds_load16(rs, stg + (rl0 + 4 * i) * STG_ROW, t * ld * 2 + 16 * c);
+    }
+}
+
+// load_perm's 8 values of staged row rl: dims 32 s + 4 g .. + 3 and 32 s + 16 + 4 g .. + 3
+__device__ __forceinline__ u32x4 staged_perm(const unsigned char* stg, int rl, int s, int g) {
+    const unsigned char* rp = stg + rl * STG_ROW + 8 * (g & 1);
+    const u32x2 a = *reinterpret_cast<const u32x2*>(rp + (((4 * s + (g >> 1)) ^ (rl & 15)) << 4));
+    const u32x2 b = *reinterpret_cast<const u32x2*>(rp + (((4 * s + 2 + (g >> 1)) ^ (rl & 15)) << 4));
+    return u32x4{a[0], a[1], b[0], b[1]};
+}
+
 __global__ void __launch_bounds__(PT)
     gdn_prep(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
              const float* __restrict__ g, const bf16* __restrict__ beta, Work ws, int T, int H, int HK, float scale,
@@ -309,19 +341,20 @@ __global__ void __launch_bounds__(PT)
     //    Every load is unconditional (rows past T read row T - 1) and the rows past T are zeroed
     //    at their first use, so no load waits for another: the gates go first, and memory waits
     //    being in issue order, the decay scan below waits only for them while the rows are in
-    //    flight.
+    //    flight. The k and q rows move to LDS as whole cache lines (a fragment's pieces are
+    //    half lines 4 KB apart), into the two 4 KB slices of the k planes that this wave alone
+    //    writes in step 2, after it has read them back in fragment order.
     const int tl = t0 + lane, tlc = min(tl, T - 1);
     const float g_raw = g[(size_t)tlc * H + h];
     const bf16 b_raw = beta[(size_t)tlc * H + h];
     __builtin_amdgcn_sched_barrier(0);
     const int qb = 3 - wave;
     const int krow = 16 * wave + col, qrow = 16 * qb + col;
+    unsigned char* const stg_k = sm + R0;                             // row r at r * 256
+    unsigned char* const stg_q = sm + R0 + PLANE + (wave - qb) * 4096;  // rows of block qb
+    stage_rows(k + (size_t)hk * DK, HK * DK, t0, 16 * wave, T, stg_k, lane);
+    stage_rows(q + (size_t)hk * DK, HK * DK, t0, 16 * qb, T, stg_q, lane);
     u32x4 kraw[4], qraw[4], vc[4];
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        kraw[s] = load_perm(k + ((size_t)min(t0 + krow, T - 1) * HK + hk) * DK, s, grp);
-        qraw[s] = load_perm(q + ((size_t)min(t0 + qrow, T - 1) * HK + hk) * DK, s, grp);
-    }
 #pragma unroll
     for (int tb_ = 0; tb_ < 4; tb_++) {
         const int t = t0 + 16 * tb_ + col;
@@ -337,7 +370,14 @@ __global__ void __launch_bounds__(PT)
         const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
         if (j <= lane) cs = cs + gj;
     }
-    // rows past T are zero from here on
+    // the staged rows (the four v loads issued after them may be in flight); rows past T are
+    // zero from here on
+    __builtin_amdgcn_s_waitcnt(0x0f74);
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        kraw[s] = staged_perm(stg_k, krow, s, grp);
+        qraw[s] = staged_perm(stg_q, qrow, s, grp);
+    }
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int s = 0; s < 4; s++) {
@@ -587,42 +627,11 @@ __global__ void __launch_bounds__(PT)
 constexpr int PT8 = 512;
 constexpr int QPL = PREP_SMEM;                         // q^ planes: hi then lo, [4 blocks][4 steps]
 // input rows staged by LDS DMA: k, q and v of the chunk, [64 rows][256 B] each
-constexpr int STG_ROW = DK * 2;
 constexpr int STG_K = QPL + 2 * PLANE;
 constexpr int STG_Q = STG_K + C * STG_ROW;
 constexpr int STG_V = STG_Q + C * STG_ROW;
 constexpr int PREP8_SMEM = STG_V + C * STG_ROW;
 static_assert(PREP8_SMEM <= 160 * 1024, "gdn_prep8 fits the LDS");
-
-// A buffer load of 16 bytes per lane straight into LDS: lane l's chunk lands at lds + 16 l.
-// (A __device__ function: the builtin used inside a kernel's lambda kept the host pass from
-// emitting the kernel's launch stub.)
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, int voff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
-}
-
-// Rows rl0 .. rl0 + 15 of a chunk (token t0 + rl at base + t ld, 256 bytes; rows past T read
-// row T - 1) into the staging area stg as whole cache lines: 16-byte chunk c of row rl sits at
-// chunk position c ^ (rl % 16), so the permuted reads of staged_perm hit distinct banks.
-__device__ __forceinline__ void stage_rows(const bf16* base, int ld, int t0, int rl0, int T, unsigned char* stg,
-                                           int lane) {
-    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(base), (short)0, 0x7fffffff, 0x00020000);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int rl = rl0 + 4 * i + (lane >> 4);
-        const int c = (lane & 15) ^ (rl & 15);
-        const int t = min(t0 + rl, T - 1);
-        lds_load16(rs, stg + (rl0 + 4 * i) * STG_ROW, t * ld * 2 + 16 * c);
-    }
-}
-
-// load_perm's 8 values of staged row rl: dims 32 s + 4 g .. + 3 and 32 s + 16 + 4 g .. + 3
-__device__ __forceinline__ u32x4 staged_perm(const unsigned char* stg, int rl, int s, int g) {
-    const unsigned char* rp = stg + rl * STG_ROW + 8 * (g & 1);
-    const u32x2 a = *reinterpret_cast<const u32x2*>(rp + (((4 * s + (g >> 1)) ^ (rl & 15)) << 4));
-    const u32x2 b = *reinterpret_cast<const u32x2*>(rp + (((4 * s + 2 + (g >> 1)) ^ (rl & 15)) << 4));
-    return u32x4{a[0], a[1], b[0], b[1]};
-}
 
 // One fragment (64 lanes x 16 or 8 bytes at frag, a wave-uniform address) stored at device
 // scope (the SC1 cache-policy bit): the line is written through the XCD's L2 instead of being
