@@ -186,6 +186,7 @@ constexpr int R0_TB = R0_TM + C * FLD * 4;         // 16640
 constexpr int R0_SC = R0_TB + C * TLD * 2;         // 25856
 constexpr int R1 = R0 + 2 * PLANE;                 // A float [64][65]; then raw k fragments
 static_assert(C * FLD * 4 >= 16 * (int)FRAG * 16, "region 1 holds the 16 raw k fragments");
+static_assert(C * FLD * 4 >= C * DK * 2, "region 1 holds the staged v rows of gdn_prep");
 constexpr int R2 = R1 + C * FLD * 4;               // cum, beta, e^cum, e^(last-cum), k inverse norm
 constexpr int PREP_SMEM = R2 + 5 * C * 4;
 static_assert(R0_SC + 4 * 256 * 4 <= R1, "region 0 overlay fits");
@@ -354,12 +355,10 @@ __global__ void __launch_bounds__(PT)
     unsigned char* const stg_q = sm + R0 + PLANE + (wave - qb) * 4096;  // rows of block qb
     stage_rows(k + (size_t)hk * DK, HK * DK, t0, 16 * wave, T, stg_k, lane);
     stage_rows(q + (size_t)hk * DK, HK * DK, t0, 16 * qb, T, stg_q, lane);
+    // the v rows 16 wave .. + 15 go to region 1 (A is written there from step 3 on); each wave
+    // reads its dim step of all 64 rows after the next block barrier
+    stage_rows(v + (size_t)h * DK, H * DK, t0, 16 * wave, T, sm + R1, lane);
     u32x4 kraw[4], qraw[4], vc[4];
-#pragma unroll
-    for (int tb_ = 0; tb_ < 4; tb_++) {
-        const int t = t0 + 16 * tb_ + col;
-        vc[tb_] = load_perm(v + ((size_t)min(t, T - 1) * H + h) * DK, wave, grp);
-    }
     __builtin_amdgcn_sched_barrier(0);
     const float gv = tl < T ? g_raw : 0.f;
     const float bv = tl < T ? f32(b_raw) : 0.f;
@@ -370,14 +369,16 @@ __global__ void __launch_bounds__(PT)
         const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
         if (j <= lane) cs = cs + gj;
     }
-    // the staged rows (the four v loads issued after them may be in flight); rows past T are
-    // zero from here on
-    __builtin_amdgcn_s_waitcnt(0x0f74);
+    // the staged rows; rows past T are zero from here on
+    wait_vm_all();
 #pragma unroll
     for (int s = 0; s < 4; s++) {
         kraw[s] = staged_perm(stg_k, krow, s, grp);
         qraw[s] = staged_perm(stg_q, qrow, s, grp);
     }
+    __syncthreads();
+#pragma unroll
+    for (int tb_ = 0; tb_ < 4; tb_++) vc[tb_] = staged_perm(sm + R1, 16 * tb_ + col, wave, grp);
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int s = 0; s < 4; s++) {
