@@ -665,17 +665,35 @@ __global__ void __launch_bounds__(512, 1)
     // Q fragments beside them, then K(1), K(2), V(0), V(1).
     dma_k(0, 0, ntg > 0);
     dma_v(-1, 3, false);
-    // Q^T (B operand): column c32, dims 16 s + 8 hh .. + 7
+    // Q^T (B operand): column c32, dims 16 s + 8 hh .. + 7. The wave's 32 (row, head) rows
+    // move to LDS as whole lines (two heads of a row are 512 contiguous bytes; read directly,
+    // a fragment takes 32 bytes of 32 rows) into the four 2 KB pieces that the wave itself
+    // fills with K(1), V(1), K(2) and V(2) once the fragments are in registers. Row-head
+    // i = 2 r + hb (row wq0 + r, head 2 pair + hb of the unit) sits at piece i / 8, row i % 8,
+    // its 16-byte chunk c at slot c ^ r.
     u32x4 qf[8];
     {
-        const bf16* qr = q + ((size_t)min(qrow, T - 1) * Hq + h) * D + 8 * hh;
+        const int rb = min(wq0, T - 1);
+        const uint64_t a = (uint64_t)(q + ((size_t)rb * Hq + unit * 4 + 2 * pair) * D);
+        const u32x4 qd = {(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                          (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) & 0xffffu, 0x7fffffffu,
+                          0x00020000u};
 #pragma unroll
-        for (int s = 0; s < 8; s++) qf[s] = ldg16(qr + 16 * s);
+        for (int n = 0; n < 8; n++) {
+            const int i = 4 * n + (lane >> 4), r = i >> 1, hb = i & 1;
+            const int voff = ((min(wq0 + r, T - 1) - rb) * Hq + hb) * D * 2 + (((lane & 15) ^ r) << 4);
+            const int p = n >> 1;
+            dma16(qd, gbase + (1 + (p >> 1)) * STAGE + (p & 1) * K_BYTES + gw * 2048 + (n & 1) * 1024, voff, 0);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const int r = c32 & 15, i = 2 * r + (c32 >> 4), p = i >> 3;
+        const unsigned char* qs = gstage + (1 + (p >> 1)) * STAGE + (p & 1) * K_BYTES + gw * 2048 + (i & 7) * ROW;
+#pragma unroll
+        for (int s = 0; s < 8; s++) qf[s] = *reinterpret_cast<const u32x4*>(qs + (((2 * s + hh) ^ r) << 4));
     }
-    // The Q fragments must be complete before the loop: an empty asm that uses them pins their
-    // loads (and the wait for them) here, so the compiler neither sinks the loads into the
-    // loop nor waits on vector memory counts there, where the transfers it does not count
-    // would turn its waits into waits for tiles in flight.
+    // The Q fragments must be complete before the loop, and read before this wave's transfers
+    // into their pieces: an empty asm that uses them pins the reads (and the wait for them)
+    // here, so the compiler neither sinks them into the loop nor waits on counts there.
 #pragma unroll
     for (int i = 0; i < 8; i++) asm volatile("" ::"v"(qf[i]));
     wait_vm_all();
