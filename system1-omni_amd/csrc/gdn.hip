@@ -713,6 +713,29 @@ __device__ __forceinline__ void prep8_p_frag(int qb, int s2, const u32x4* khi_pl
     store_through(&ws.pb[(rec * 8 + qb * 2 + s2) * FRAG], lane, pack_pair(pt[0], pt[1]));
 }
 
+// Diagonal block (base, base) of T = (I + A)^-1 by forward substitution, column cc on lane cc,
+// with the block's 120 strictly-lower entries of A read from LDS into registers before the
+// first product, so the substitution does not wait on the LDS along its chain (the same
+// products and sums, in the same order, as reading each entry where it is used).
+__device__ __forceinline__ void diag_inverse_preloaded(const float* am, float* tm, int base, int cc) {
+    float a[120];
+#pragma unroll
+    for (int r = 1, n = 0; r < 16; r++)
+#pragma unroll
+        for (int j = 0; j < r; j++, n++) a[n] = am[(base + r) * FLD + base + j];
+    __builtin_amdgcn_sched_barrier(0);
+    float xs[16];
+#pragma unroll
+    for (int r = 0, n = 0; r < 16; r++) {
+        float acc = r == cc ? 1.f : 0.f;
+#pragma unroll
+        for (int j = 0; j < r; j++, n++) acc = fmaf(-a[n], xs[j], acc);
+        xs[r] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) tm[(base + r) * FLD + base + cc] = xs[r];
+}
+
 __global__ void __launch_bounds__(PT8)
     gdn_prep8(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
               const float* __restrict__ g, const bf16* __restrict__ beta, Work ws, int T, int H, int HK, float scale,
@@ -968,19 +991,7 @@ __global__ void __launch_bounds__(PT8)
             }
         }
     };
-    if (kside && lane < 16) {
-        const int base = 16 * blk, cc = lane;
-        float xs[16];
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            float acc = r == cc ? 1.f : 0.f;
-#pragma unroll
-            for (int j = 0; j < r; j++) acc = fmaf(-am[(base + r) * FLD + base + j], xs[j], acc);
-            xs[r] = acc;
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r++) tm[(base + r) * FLD + base + cc] = xs[r];
-    }
+    if (kside && lane < 16) diag_inverse_preloaded(am, tm, 16 * blk, lane);
     __syncthreads();
     Q35_PHASE(4);
     if (!kside) transposes();
