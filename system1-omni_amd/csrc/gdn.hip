@@ -239,8 +239,10 @@ __device__ unsigned long long q35_wave_ticks[64];
 // level's trip counts are constants, so every operand is read from LDS ahead of the MFMA chain
 // (the products and their order are those of a loop over the blocks). The partial product
 // passes through the wave's own scratch, whose writes precede its reads in the wave's LDS order.
+// The block goes to T (float) and to Tb = bf16(T_ij beta_j), the scan operand's factor.
 template <int LV>
-__device__ __forceinline__ void inverse_level(int bi, const float* am, float* tm, float* scr, int col, int grp) {
+__device__ __forceinline__ void inverse_level(int bi, const float* am, float* tm, bf16* tb, const float* bet,
+                                              float* scr, int col, int grp) {
     const int bj = bi - LV;
     float a[4 * LV], t[4 * LV], tii[4];
 #pragma unroll
@@ -261,8 +263,12 @@ __device__ __forceinline__ void inverse_level(int bi, const float* am, float* tm
     acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) acc = mfma_f32(tii[kk], scr[(4 * kk + grp) * 16 + col], acc);
+    const float bj_beta = bet[16 * bj + col];
 #pragma unroll
-    for (int r = 0; r < 4; r++) tm[(16 * bi + 4 * grp + r) * FLD + 16 * bj + col] = -acc[r];
+    for (int r = 0; r < 4; r++) {
+        tm[(16 * bi + 4 * grp + r) * FLD + 16 * bj + col] = -acc[r];
+        tb[(16 * bi + 4 * grp + r) * TLD + 16 * bj + col] = to_bf16(-acc[r] * bj_beta);
+    }
 }
 
 constexpr int STG_ROW = DK * 2;  // bytes of a staged input row
@@ -508,14 +514,17 @@ __global__ void __launch_bounds__(PT)
 
     // 4. T = (I + A)^-1. Upper off-diagonal blocks are zero; the diagonal blocks by forward
     //    substitution in the reference order (wave w, lanes 0..15: one column each).
+    //    Each block of T is written with its Tb = bf16(T_ij beta_j) as it is produced.
     for (int x = tid; x < 6 * 256; x += PT) {
         const int blk = x / 256, r = (x % 256) / 16, cc = x % 16;
         const int bi = blk < 3 ? 0 : blk < 5 ? 1 : 2;
         const int bj = blk < 3 ? blk + 1 : blk < 5 ? blk - 1 : 3;
         tm[(16 * bi + r) * FLD + 16 * bj + cc] = 0.f;
+        tb[(16 * bi + r) * TLD + 16 * bj + cc] = 0;
     }
     if (lane < 16) {
         const int base = 16 * wave, cc = lane;
+        const float beta_c = bet[base + cc];
         float xs[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -525,26 +534,25 @@ __global__ void __launch_bounds__(PT)
             xs[r] = acc;
         }
 #pragma unroll
-        for (int r = 0; r < 16; r++) tm[(base + r) * FLD + base + cc] = xs[r];
+        for (int r = 0; r < 16; r++) {
+            tm[(base + r) * FLD + base + cc] = xs[r];
+            tb[(base + r) * TLD + base + cc] = to_bf16(xs[r] * beta_c);
+        }
     }
     __syncthreads();
     Q35_PHASE(4);
     //    the off-diagonal levels, wave bi computing T_{bi, bi - lv}
-    if (wave >= 1) inverse_level<1>(wave, am, tm, scr, col, grp);
+    if (wave >= 1) inverse_level<1>(wave, am, tm, tb, bet, scr, col, grp);
     __syncthreads();
-    if (wave >= 2) inverse_level<2>(wave, am, tm, scr, col, grp);
+    if (wave >= 2) inverse_level<2>(wave, am, tm, tb, bet, scr, col, grp);
     __syncthreads();
-    if (wave >= 3) inverse_level<3>(wave, am, tm, scr, col, grp);
+    if (wave >= 3) inverse_level<3>(wave, am, tm, tb, bet, scr, col, grp);
     __syncthreads();
     Q35_PHASE(5);
 
-    // 5. Tb = bf16(T beta_j); the raw k rows go to region 1 (A is dead) for step 6
+    // 5. the raw k rows go to region 1 (A is dead) for step 6
 #pragma unroll
     for (int s = 0; s < 4; s++) reinterpret_cast<u32x4*>(am)[(wave * 4 + s) * FRAG + lane] = kraw[s];
-    for (int x = tid; x < C * C; x += PT) {
-        const int i = x / C, j = x % C;
-        tb[i * TLD + j] = to_bf16(tm[i * FLD + j] * bet[j]);
-    }
     __syncthreads();
     Q35_PHASE(6);
 
@@ -713,11 +721,12 @@ __device__ __forceinline__ void prep8_p_frag(int qb, int s2, const u32x4* khi_pl
     store_through(&ws.pb[(rec * 8 + qb * 2 + s2) * FRAG], lane, pack_pair(pt[0], pt[1]));
 }
 
-// Diagonal block (base, base) of T = (I + A)^-1 by forward substitution, column cc on lane cc,
+// Diagonal block (base, base) of T = (I + A)^-1 (and of Tb) by forward substitution, column cc on lane cc,
 // with the block's 120 strictly-lower entries of A read from LDS into registers before the
 // first product, so the substitution does not wait on the LDS along its chain (the same
 // products and sums, in the same order, as reading each entry where it is used).
-__device__ __forceinline__ void diag_inverse_preloaded(const float* am, float* tm, int base, int cc) {
+__device__ __forceinline__ void diag_inverse_preloaded(const float* am, float* tm, bf16* tb, const float* bet, int base,
+                                                       int cc) {
     float a[120];
 #pragma unroll
     for (int r = 1, n = 0; r < 16; r++)
@@ -732,8 +741,12 @@ __device__ __forceinline__ void diag_inverse_preloaded(const float* am, float* t
         for (int j = 0; j < r; j++, n++) acc = fmaf(-a[n], xs[j], acc);
         xs[r] = acc;
     }
+    const float beta_c = bet[base + cc];
 #pragma unroll
-    for (int r = 0; r < 16; r++) tm[(base + r) * FLD + base + cc] = xs[r];
+    for (int r = 0; r < 16; r++) {
+        tm[(base + r) * FLD + base + cc] = xs[r];
+        tb[(base + r) * TLD + base + cc] = to_bf16(xs[r] * beta_c);
+    }
 }
 
 __global__ void __launch_bounds__(PT8)
@@ -921,6 +934,7 @@ __global__ void __launch_bounds__(PT8)
         case 3:
             prep8_a_tile(1, 0, khi_pl, klo_pl, am, cum, bet, lane);
             prep8_p_frag(0, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+            prep8_p_frag(2, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
             break;
         case 4:
             prep8_p_frag(3, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
@@ -930,7 +944,6 @@ __global__ void __launch_bounds__(PT8)
             break;
         case 6:
             prep8_p_frag(2, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
-            prep8_p_frag(2, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
             break;
         default:
             prep8_p_frag(1, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
@@ -953,6 +966,7 @@ __global__ void __launch_bounds__(PT8)
         const int bi = blk_ < 3 ? 0 : blk_ < 5 ? 1 : 2;
         const int bj = blk_ < 3 ? blk_ + 1 : blk_ < 5 ? blk_ - 1 : 3;
         tm[(16 * bi + r) * FLD + 16 * bj + cc] = 0.f;
+        tb[(16 * bi + r) * TLD + 16 * bj + cc] = 0;
     }
     // step 6's transposes of dim step ds = wave & 3: q side the kd fragments (stored) and v,
     // k side kw, into f[token step][half] (fvt or fkw)
@@ -991,29 +1005,23 @@ __global__ void __launch_bounds__(PT8)
             }
         }
     };
-    if (kside && lane < 16) diag_inverse_preloaded(am, tm, 16 * blk, lane);
+    if (kside && lane < 16) diag_inverse_preloaded(am, tm, tb, bet, 16 * blk, lane);
     __syncthreads();
     Q35_PHASE(4);
     if (!kside) transposes();
     float* scr = reinterpret_cast<float*>(sm + R0_SC) + blk * 256;
-    if (kside && blk >= 1) inverse_level<1>(blk, am, tm, scr, col, grp);
+    if (kside && blk >= 1) inverse_level<1>(blk, am, tm, tb, bet, scr, col, grp);
     __syncthreads();
-    if (kside && blk >= 2) inverse_level<2>(blk, am, tm, scr, col, grp);
+    if (kside && blk >= 2) inverse_level<2>(blk, am, tm, tb, bet, scr, col, grp);
     __syncthreads();
-    if (kside && blk >= 3) inverse_level<3>(blk, am, tm, scr, col, grp);
+    if (kside && blk >= 3) inverse_level<3>(blk, am, tm, tb, bet, scr, col, grp);
     __syncthreads();
     Q35_PHASE(5);
 
-    // 5. Tb = bf16(T beta_j)
-    for (int x = tid; x < C * C; x += PT8) {
-        const int i = x / C, j = x % C;
-        tb[i * TLD + j] = to_bf16(tm[i * FLD + j] * bet[j]);
-    }
-    __syncthreads();
     Q35_PHASE(6);
 
-    // 6. u = Tb v on the q side (its transposes ran in step 4); on the k side the kw transpose
-    //    and w^T = kw^T Tb^T
+    // 6. (Tb was written with T in step 4) u = Tb v on the q side (its transposes ran in step 4);
+    //    on the k side the kw transpose and w^T = kw^T Tb^T
     if (kside) transposes();
 #pragma unroll
     for (int it = 0; it < 4; it++) {
