@@ -351,9 +351,17 @@ __global__ void __launch_bounds__(PT)
     //    flight. The k and q rows move to LDS as whole cache lines (a fragment's pieces are
     //    half lines 4 KB apart), into the two 4 KB slices of the k planes that this wave alone
     //    writes in step 2, after it has read them back in fragment order.
-    const int tl = t0 + lane, tlc = min(tl, T - 1);
-    const float g_raw = g[(size_t)tlc * H + h];
-    const bf16 b_raw = beta[(size_t)tlc * H + h];
+    //    Wave 0 alone loads the gates (by hand, and waits for them by hand: as ordinary loads
+    //    under a branch the compiler placed them, or the wait for them, after the row
+    //    transfers) and computes the decay for the block.
+    const int tl = t0 + lane;
+    float g_raw = 0.f;
+    uint32_t b_bits = 0;
+    if (wave == 0) {
+        const int tlc = min(tl, T - 1);
+        asm volatile("global_load_dword %0, %1, off" : "=v"(g_raw) : "v"(g + (size_t)tlc * H + h));
+        asm volatile("global_load_ushort %0, %1, off" : "=v"(b_bits) : "v"(beta + (size_t)tlc * H + h));
+    }
     __builtin_amdgcn_sched_barrier(0);
     const int qb = 3 - wave;
     const int krow = 16 * wave + col, qrow = 16 * qb + col;
@@ -366,14 +374,23 @@ __global__ void __launch_bounds__(PT)
     stage_rows(v + (size_t)h * DK, H * DK, t0, 16 * wave, T, sm + R1, lane);
     u32x4 kraw[4], qraw[4], vc[4];
     __builtin_amdgcn_sched_barrier(0);
-    const float gv = tl < T ? g_raw : 0.f;
-    const float bv = tl < T ? f32(b_raw) : 0.f;
 
-    // 1. cumulative log-decay, in index order (every wave, lane = token)
-    float cs = 0.f;
-    for (int j = 0; j < C; j++) {
-        const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
-        if (j <= lane) cs = cs + gj;
+    // 1. cumulative log-decay, in index order (wave 0, lane = token), published through LDS
+    //    at the barrier below
+    if (wave == 0) {
+        asm volatile("s_waitcnt vmcnt(12)" : "+v"(g_raw), "+v"(b_bits));  // the 12 row transfers may be in flight
+        const float gv = tl < T ? g_raw : 0.f;
+        const float bv = tl < T ? __uint_as_float(b_bits << 16) : 0.f;
+        float cs = 0.f;
+        for (int j = 0; j < C; j++) {
+            const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
+            if (j <= lane) cs = cs + gj;
+        }
+        const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs), C - 1));
+        cum[lane] = cs;
+        bet[lane] = bv;
+        ecum[lane] = expf(cs);
+        erem[lane] = expf(last - cs);
     }
     // the staged rows; rows past T are zero from here on
     wait_vm_all();
@@ -394,15 +411,6 @@ __global__ void __launch_bounds__(PT)
 #pragma unroll
     for (int tb_ = 0; tb_ < 4; tb_++)
         if (t0 + 16 * tb_ + col >= T) vc[tb_] = zero4;
-    const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs), C - 1));
-    const float ec = expf(cs), er = expf(last - cs);
-    if (wave == 0) {
-        cum[lane] = cs;
-        bet[lane] = bv;
-        ecum[lane] = ec;
-        erem[lane] = er;
-        if (lane == C - 1) ws.decay[rec] = expf(cs);
-    }
     Q35_PHASE(1);
 
     // 2. L2 norms (row sums over the 4 lane groups), TF32 split of k^, q^ and qd
@@ -424,7 +432,7 @@ __global__ void __launch_bounds__(PT)
     qs += __shfl_xor(qs, 32, 64);
     const float kinv = rsqrtf(ks + 1e-6f), qinv = rsqrtf(qs + 1e-6f) * scale;
     if (grp == 0) kinv_s[krow] = kinv;
-    const float ecq = __shfl(ec, qrow, 64);
+    const float ecq = ecum[qrow];
     u32x4 khi[4], klo[4], qhi[4], qlo[4];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
@@ -613,6 +621,8 @@ __global__ void __launch_bounds__(PT)
         }
         ws.w[(rec * 16 + it * 4 + wave) * FRAG + lane] = pack_pair(wt[0], wt[1]);
     }
+    // the chunk's decay, stored last: a store before a block barrier is waited for there
+    if (wave == 0 && lane == C - 1) ws.decay[rec] = ecum[C - 1];
     Q35_PHASE(7);
 }
 
