@@ -30,7 +30,10 @@ __global__ void __launch_bounds__(THREADS) embed_rows(const int32_t* __restrict_
 
 // ---- causal depthwise conv1d (k = 4) + SiLU ----
 
-constexpr int CONV_RUN = 16;  // tokens per thread
+constexpr int CONV_RUN = 16;       // tokens per thread (each run also reads the 3 rows before it)
+constexpr int CONV_RUN_LONG = 32;  // for launches with threads to spare: less history re-read
+constexpr size_t CONV_LONG_MIN_THREADS = 65536;
+constexpr int CONV_BATCH = 8;      // rows loaded ahead, a batch before the previous one's stores
 
 __device__ __forceinline__ void conv_store(bf16* q, bf16* k, bf16* v, int key_dim, int value_dim, int t, int c,
                                            const Pack8& y) {
@@ -54,15 +57,16 @@ struct ConvSeqs {
     const bf16* hist;
 };
 
-// One thread owns 8 consecutive channels for CONV_RUN consecutive tokens. Requires
+// One thread owns 8 consecutive channels for RUN consecutive tokens. Requires
 // 8 | key_dim, 8 | value_dim, 8 | ld and 16-byte aligned buffers (checked by the host).
+template <int RUN>
 __global__ void __launch_bounds__(THREADS)
     gdn_conv_vec_kernel(const bf16* __restrict__ qkv, int ld, const bf16* __restrict__ w, bf16* __restrict__ q,
                         bf16* __restrict__ k, bf16* __restrict__ v, int T, int key_dim, int value_dim,
                         const ConvSeqs sq) {
     const int packs = (2 * key_dim + value_dim) / 8;
     const int idx = blockIdx.x * THREADS + threadIdx.x;
-    const int runs = sq.n > 0 ? sq.run[sq.n] : (T + CONV_RUN - 1) / CONV_RUN;
+    const int runs = sq.n > 0 ? sq.run[sq.n] : (T + RUN - 1) / RUN;
     if (idx >= packs * runs) return;
     const int cp = idx % packs;
     int run = idx / packs;
@@ -80,7 +84,7 @@ __global__ void __launch_bounds__(THREADS)
         v += (size_t)r0 * value_dim;
         hist = sq.hist;
     }
-    const int c = cp * 8, t0 = run * CONV_RUN;
+    const int c = cp * 8, t0 = run * RUN;
     float wt[8][4];
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
@@ -107,10 +111,10 @@ __global__ void __launch_bounds__(THREADS)
             for (int i = 0; i < 8; i++) win[r][i] = 0.f;
         }
     }
-    const int t_end = min(T, t0 + CONV_RUN);
-    for (int t = t0; t < t_end; t++) {
+    const int t_end = min(T, t0 + RUN);
+    auto one_row = [&](int t, const Pack8& raw) {
         float cur[8];
-        unpack8(*reinterpret_cast<const Pack8*>(qkv + (size_t)t * ld + c), cur);
+        unpack8(raw, cur);
         float y[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -129,7 +133,31 @@ __global__ void __launch_bounds__(THREADS)
             win[1][i] = win[2][i];
             win[2][i] = cur[i];
         }
+    };
+    // a whole run: batch b + 1's loads are issued before batch b's stores (a fixed schedule,
+    // fully unrolled), so a thread keeps a batch of loads in flight instead of one row
+    int t = t0;
+    if (t0 + RUN <= t_end) {
+        Pack8 cur_b[CONV_BATCH], next_b[CONV_BATCH];
+#pragma unroll
+        for (int u = 0; u < CONV_BATCH; u++) cur_b[u] = *reinterpret_cast<const Pack8*>(qkv + (size_t)(t0 + u) * ld + c);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int bt = 0; bt < RUN / CONV_BATCH; bt++) {
+            if (bt + 1 < RUN / CONV_BATCH) {
+#pragma unroll
+                for (int u = 0; u < CONV_BATCH; u++)
+                    next_b[u] = *reinterpret_cast<const Pack8*>(qkv + (size_t)(t0 + (bt + 1) * CONV_BATCH + u) * ld + c);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // the batch's loads stay ahead of this batch's rows
+#pragma unroll
+            for (int u = 0; u < CONV_BATCH; u++) one_row(t0 + bt * CONV_BATCH + u, cur_b[u]);
+#pragma unroll
+            for (int u = 0; u < CONV_BATCH; u++) cur_b[u] = next_b[u];
+        }
+        t = t_end;
     }
+    for (; t < t_end; t++) one_row(t, *reinterpret_cast<const Pack8*>(qkv + (size_t)t * ld + c));
 }
 
 // Any shape (unaligned buffers or channel counts not a multiple of 8): one thread per
@@ -305,13 +333,20 @@ extern "C" int cs1_gdn_conv(const void* qkv, int ld, const void* w, void* q, voi
     const bool vec = key_dim % 8 == 0 && value_dim % 8 == 0 && ld % 8 == 0 && aligned16(qkv) && aligned16(w) &&
                      aligned16(q) && aligned16(k) && aligned16(v);
     if (vec) {
-        const size_t threads = (size_t)(channels / 8) * ((T + CONV_RUN - 1) / CONV_RUN);
         ConvSeqs one;
         one.n = 0;
         one.hist = nullptr;
-        gdn_conv_vec_kernel<<<cdiv(threads, THREADS), THREADS, 0, st>>>(
-            static_cast<const bf16*>(qkv), ld, static_cast<const bf16*>(w), static_cast<bf16*>(q),
-            static_cast<bf16*>(k), static_cast<bf16*>(v), T, key_dim, value_dim, one);
+        const size_t threads_long = (size_t)(channels / 8) * ((T + CONV_RUN_LONG - 1) / CONV_RUN_LONG);
+        if (threads_long >= CONV_LONG_MIN_THREADS) {
+            gdn_conv_vec_kernel<CONV_RUN_LONG><<<cdiv(threads_long, THREADS), THREADS, 0, st>>>(
+                static_cast<const bf16*>(qkv), ld, static_cast<const bf16*>(w), static_cast<bf16*>(q),
+                static_cast<bf16*>(k), static_cast<bf16*>(v), T, key_dim, value_dim, one);
+        } else {
+            const size_t threads = (size_t)(channels / 8) * ((T + CONV_RUN - 1) / CONV_RUN);
+            gdn_conv_vec_kernel<CONV_RUN><<<cdiv(threads, THREADS), THREADS, 0, st>>>(
+                static_cast<const bf16*>(qkv), ld, static_cast<const bf16*>(w), static_cast<bf16*>(q),
+                static_cast<bf16*>(k), static_cast<bf16*>(v), T, key_dim, value_dim, one);
+        }
     } else {
         const size_t threads = (size_t)channels * ((T + CONV_RUN - 1) / CONV_RUN);
         gdn_conv_any_kernel<<<cdiv(threads, THREADS), THREADS, 0, st>>>(
@@ -344,7 +379,7 @@ extern "C" int cs1_gdn_conv_varlen(const void* qkv, int ld, const void* w, void*
     const size_t threads = (size_t)((2 * key_dim + value_dim) / 8) * sq.run[nseq];
     if (threads == 0) return hipSuccess;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    gdn_conv_vec_kernel<<<cdiv(threads, THREADS), THREADS, 0, st>>>(
+    gdn_conv_vec_kernel<CONV_RUN><<<cdiv(threads, THREADS), THREADS, 0, st>>>(
         static_cast<const bf16*>(qkv), ld, static_cast<const bf16*>(w), static_cast<bf16*>(q), static_cast<bf16*>(k),
         static_cast<bf16*>(v), cu_seqlens[nseq], key_dim, value_dim, sq);
     return hipGetLastError();
