@@ -796,6 +796,10 @@ __global__ void __launch_bounds__(PT8)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool kside = wave < 4;
     const int blk = wave & 3;  // k row block (k side) / q row block and v dim step (q side)
+    // role: 0 = the whole item; split launches (gridDim.z = 2) give each item two blocks,
+    // 1 = A, the inverse, w, u and kd (waves 4-7 move v instead of q), 2 = qd and pb
+    const int role = gridDim.z == 1 ? 0 : 1 + (int)blockIdx.z;
+    const bool has_q = role != 1, has_t = role != 2;
     const size_t rec = (size_t)h * NC + c;
     const int t0 = cl * C;
     Q35_PHASE_START();
@@ -819,7 +823,10 @@ __global__ void __launch_bounds__(PT8)
     }
     __builtin_amdgcn_sched_barrier(0);
     unsigned char* const stg = sm + (kside ? STG_K : STG_Q);
-    stage_rows((kside ? k : q) + (size_t)hk * DK, HK * DK, t0, 16 * blk, T, stg, lane);
+    if (kside || has_q)
+        stage_rows((kside ? k : q) + (size_t)hk * DK, HK * DK, t0, 16 * blk, T, stg, lane);
+    else
+        stage_rows(v + (size_t)h * DK, H * DK, t0, 16 * blk, T, sm + STG_V, lane);
     __builtin_amdgcn_sched_barrier(0);
 
     // 1. cumulative log-decay on wave 3 alone (lane = token), published through LDS for step
@@ -849,16 +856,19 @@ __global__ void __launch_bounds__(PT8)
     // the next barrier. Rows past T are zero from here on.
     wait_vm_all();
     u32x4 raw[4], vc[4];
+    const bool has_rows = kside || has_q;
+    if (has_rows) {
 #pragma unroll
-    for (int s = 0; s < 4; s++) raw[s] = staged_perm(stg, row, s, grp);
-    if (!kside) stage_rows(v + (size_t)h * DK, H * DK, t0, 16 * blk, T, sm + STG_V, lane);
+        for (int s = 0; s < 4; s++) raw[s] = staged_perm(stg, row, s, grp);
+    }
+    if (!kside && role == 0) stage_rows(v + (size_t)h * DK, H * DK, t0, 16 * blk, T, sm + STG_V, lane);
 #pragma unroll
     for (int s = 0; s < 4; s++)
         if (t0 + row >= T) raw[s] = u32x4{0u, 0u, 0u, 0u};
 
     // 2. L2 norms and TF32 splits: k side -> k planes, q side -> q planes
     float qinv = 0.f;
-    {
+    if (has_rows) {
         float ss = 0.f;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
@@ -901,17 +911,19 @@ __global__ void __launch_bounds__(PT8)
         }
     }
     Q35_WSTAMP(3);
-    if (!kside) wait_vm_all();  // the staged v rows
+    if (!kside && has_t) wait_vm_all();  // the staged v rows
     __syncthreads();
     Q35_PHASE(2);
     Q35_WSTAMP(4);
     // qd = (q^ scale) e^cum once the cumulative decay is in LDS
-    if (!kside) {
+    if (!kside && has_t) {
 #pragma unroll
         for (int tb_ = 0; tb_ < 4; tb_++) {
             vc[tb_] = staged_perm(sm + STG_V, 16 * tb_ + col, blk, grp);
             if (t0 + 16 * tb_ + col >= T) vc[tb_] = u32x4{0u, 0u, 0u, 0u};
         }
+    }
+    if (!kside && has_q) {
         const float ecq = ecum[row];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
@@ -924,40 +936,97 @@ __global__ void __launch_bounds__(PT8)
     }
 
     // 3. pair products by table: 10 A tiles and the 6 pb fragments that are not all zero (the
-    //    scan never reads fragment 1 of row blocks 0 and 1) over 8 waves
-    switch (wave) {
-        case 0:
-            prep8_a_tile(3, 3, khi_pl, klo_pl, am, cum, bet, lane);
-            prep8_a_tile(3, 2, khi_pl, klo_pl, am, cum, bet, lane);
-            prep8_a_tile(0, 0, khi_pl, klo_pl, am, cum, bet, lane);
-            break;
-        case 1:
-            prep8_a_tile(3, 1, khi_pl, klo_pl, am, cum, bet, lane);
-            prep8_a_tile(3, 0, khi_pl, klo_pl, am, cum, bet, lane);
-            prep8_a_tile(1, 1, khi_pl, klo_pl, am, cum, bet, lane);
-            break;
-        case 2:
-            prep8_a_tile(2, 2, khi_pl, klo_pl, am, cum, bet, lane);
-            prep8_a_tile(2, 1, khi_pl, klo_pl, am, cum, bet, lane);
-            prep8_a_tile(2, 0, khi_pl, klo_pl, am, cum, bet, lane);
-            break;
-        case 3:
-            prep8_a_tile(1, 0, khi_pl, klo_pl, am, cum, bet, lane);
-            prep8_p_frag(0, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
-            prep8_p_frag(2, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
-            break;
-        case 4:
-            prep8_p_frag(3, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
-            break;
-        case 5:
-            prep8_p_frag(3, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
-            break;
-        case 6:
-            prep8_p_frag(2, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
-            break;
-        default:
-            prep8_p_frag(1, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
-            break;
+    //    scan never reads fragment 1 of row blocks 0 and 1) over 8 waves, or each set over the
+    //    8 waves of its own block in a split launch
+    if (role == 0) {
+        switch (wave) {
+            case 0:
+                prep8_a_tile(3, 3, khi_pl, klo_pl, am, cum, bet, lane);
+                prep8_a_tile(3, 2, khi_pl, klo_pl, am, cum, bet, lane);
+                prep8_a_tile(0, 0, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            case 1:
+                prep8_a_tile(3, 1, khi_pl, klo_pl, am, cum, bet, lane);
+                prep8_a_tile(3, 0, khi_pl, klo_pl, am, cum, bet, lane);
+                prep8_a_tile(1, 1, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            case 2:
+                prep8_a_tile(2, 2, khi_pl, klo_pl, am, cum, bet, lane);
+                prep8_a_tile(2, 1, khi_pl, klo_pl, am, cum, bet, lane);
+                prep8_a_tile(2, 0, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            case 3:
+                prep8_a_tile(1, 0, khi_pl, klo_pl, am, cum, bet, lane);
+                prep8_p_frag(0, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                prep8_p_frag(2, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            case 4:
+                prep8_p_frag(3, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            case 5:
+                prep8_p_frag(3, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            case 6:
+                prep8_p_frag(2, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            default:
+                prep8_p_frag(1, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+        }
+    } else if (role == 1) {
+        // the 10 A tiles over the 8 waves
+        switch (wave) {
+            case 0:
+                prep8_a_tile(3, 3, khi_pl, klo_pl, am, cum, bet, lane);
+                prep8_a_tile(0, 0, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            case 1:
+                prep8_a_tile(3, 2, khi_pl, klo_pl, am, cum, bet, lane);
+                prep8_a_tile(1, 1, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            case 2:
+                prep8_a_tile(3, 1, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            case 3:
+                prep8_a_tile(3, 0, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            case 4:
+                prep8_a_tile(2, 2, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            case 5:
+                prep8_a_tile(2, 1, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            case 6:
+                prep8_a_tile(2, 0, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+            default:
+                prep8_a_tile(1, 0, khi_pl, klo_pl, am, cum, bet, lane);
+                break;
+        }
+    } else {
+        // the 6 pb fragments, one per wave; this block's work ends here
+        switch (wave) {
+            case 0:
+                prep8_p_frag(0, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            case 1:
+                prep8_p_frag(1, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            case 2:
+                prep8_p_frag(2, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            case 3:
+                prep8_p_frag(2, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            case 4:
+                prep8_p_frag(3, 0, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            case 5:
+                prep8_p_frag(3, 1, khi_pl, klo_pl, qhi_pl, qlo_pl, cum, ws, rec, lane);
+                break;
+            default: break;
+        }
+        return;
     }
     Q35_WSTAMP(5);
     __syncthreads();
@@ -1055,7 +1124,7 @@ __global__ void __launch_bounds__(PT8)
         if (kside) store_through(&ws.w[(rec * 16 + it * 4 + ds) * FRAG], lane, pack_pair(wt[0], wt[1]));
     }
     // the chunk's decay, stored last: a store before a block barrier is waited for there
-    if (wave == 3 && lane == C - 1) ws.decay[rec] = ecum[C - 1];
+    if (wave == 3 && lane == C - 1) ws.decay[rec] = ecum[C - 1];  // (role 0 or 1)
     Q35_PHASE(7);
     Q35_WSTAMP(6);
     Q35_WFLUSH();
@@ -1498,6 +1567,17 @@ bool prep_wide(long items) {
     return cus > 0 && items <= cus;
 }
 
+// gdn_prep8 as two blocks per item (the inverse path and the q side on CUs of their own) when
+// twice the items still fit the device. Overridable for tests by Q35_PREP_SPLIT (0 or 1).
+bool prep_split(long items) {
+    if (const char* e = getenv("Q35_PREP_SPLIT")) {
+        if (e[0] == '0') return false;
+        if (e[0] == '1') return true;
+    }
+    const int cus = device_cus();
+    return cus > 0 && 2 * items <= cus;
+}
+
 // Halves per scan block: one 8-wave scan block fits a CU, so `units` (heads x sequences)
 // blocks of NSUB halves run in ceil(units * 8 / NSUB / CUs) rounds. The two-half block's chunk
 // step is ~1.46x the one-half block's (measured alone on the device: 1.24 vs 0.85 us), so it
@@ -1546,9 +1626,10 @@ int gdn_launch(const void* q, const void* k, const void* v, const float* g, cons
         static const hipError_t configured8 = hipFuncSetAttribute(
             reinterpret_cast<const void*>(gdn_prep8), hipFuncAttributeMaxDynamicSharedMemorySize, PREP8_SMEM);
         if (configured8 != hipSuccess) return configured8;
-        gdn_prep8<<<dim3(NC, H), PT8, PREP8_SMEM, st>>>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
-                                                        static_cast<const bf16*>(v), g, static_cast<const bf16*>(beta),
-                                                        ws, T, H, HK, scale, gs);
+        const int roles = prep_split((long)NC * H) ? 2 : 1;
+        gdn_prep8<<<dim3(NC, H, roles), PT8, PREP8_SMEM, st>>>(static_cast<const bf16*>(q),
+                                                               static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                                                               g, static_cast<const bf16*>(beta), ws, T, H, HK, scale, gs);
     } else {
         gdn_prep<<<dim3(NC, H), PT, PREP_SMEM, st>>>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
                                                      static_cast<const bf16*>(v), g, static_cast<const bf16*>(beta), ws,

@@ -219,8 +219,9 @@ def test_gdn_scan_output_sets_are_bit_identical(t, h, hk, varlen, monkeypatch):
 @pytest.mark.parametrize("t,h,hk", [(512, 16, 16), (130, 6, 3), (107, 48, 16), (64, 8, 4)])
 def test_gdn_prep_forms_are_bit_identical(t, h, hk, monkeypatch):
     """Launches whose chunks all fit on the device at once run the 8-wave prep (gdn_prep8),
-    the others the 4-wave one; both must write the same records. The workspace starts as NaN
-    bytes each time, so a record one form leaves unwritten shows up as a difference."""
+    as two blocks per chunk when twice as many fit, the others the 4-wave one; every form must
+    write the same records. The workspace starts as NaN bytes each time, so a record one form
+    leaves unwritten shows up as a difference."""
     api, st = hip.api(), stream()
     say(f"gdn prep forms t={t} h={h} hk={hk}")
     q, k, v, g, b, s0 = cfg0_inputs(t, h, hk, seed=8, s0_std=0.01)
@@ -228,16 +229,18 @@ def test_gdn_prep_forms_are_bit_identical(t, h, hk, monkeypatch):
     si = dev(s0)
     nws = api.cs1_gdn_workspace_floats(t, h)
     runs = []
-    for wide in ("0", "1"):
+    for wide, split in (("0", "0"), ("1", "0"), ("1", "1")):
         monkeypatch.setenv("Q35_PREP_WIDE", wide)
+        monkeypatch.setenv("Q35_PREP_SPLIT", split)
         ws = dev(np.full(nws, 0xFFFFFFFF, np.uint32))
         o, so = empty(t * h * D * 2), empty(h * D * D * 4)
         hip.check(api.cs1_gdn_prefill_x(*(x.at(0) for x in bufs), o.at(0), ws.at(0), t, h, hk, D ** -0.5, si.at(0),
                                         so.at(0), st.handle), "gdn prefill")
         runs.append((get_bf16(o, t * h * D), get(so, np.float32, h * D * D), get(ws, np.uint32, nws)))
-    np.testing.assert_array_equal(runs[0][0], runs[1][0])
-    np.testing.assert_array_equal(runs[0][1], runs[1][1])
-    np.testing.assert_array_equal(runs[0][2], runs[1][2])  # every record byte
+    for other in runs[1:]:
+        np.testing.assert_array_equal(runs[0][0], other[0])
+        np.testing.assert_array_equal(runs[0][1], other[1])
+        np.testing.assert_array_equal(runs[0][2], other[2])  # every record byte
 
 
 def test_gdn_empty_window_captures_state_copy_and_zero_initial_state():
