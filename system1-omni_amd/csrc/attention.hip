@@ -607,6 +607,8 @@ __global__ void __launch_bounds__(512, 1)
     // wave = 4 kg + 2 rh + pair: key group kg, row half rh, head pair
     const int kg = __builtin_amdgcn_readfirstlane(wave >> 2), gw = __builtin_amdgcn_readfirstlane(wave & 3);
     const int rh = gw >> 1, pair = gw & 1;
+    // key group 0's waves lead on the SIMD they share with key group 1's
+    if (kg == 0) __builtin_amdgcn_s_setprio(1);
     const int c32 = lane & 31, hh = lane >> 5;  // query column, lane half
     const int units = Hq / 4;
     const int nblk = (T - q_base + ROWS - 1) / ROWS;
