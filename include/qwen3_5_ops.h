@@ -227,6 +227,23 @@ int cs1_gdn_prefill_varlen(const void* q, const void* k, const void* v, const fl
                            float* workspace, const int32_t* cu_seqlens, int nseq, int H, int HK, float scale,
                            const void* s_in, size_t s_in_stride, void* s_out, size_t s_out_stride, void* stream);
 
+/* Gated forms of cs1_gdn_prefill_x and cs1_gdn_prefill_varlen (no reference counterpart:
+ * they fold the reference's separate gates launch, cs1_gdn_gates / gdn_gates_kernel at
+ * elementwise.cu:42-55 and 115-124, into the GDN prep).  Instead of g and beta they take the
+ * raw projections b and a (bf16; token t, head h at b[t * ld + h], a[t * ld + h], ld >= H)
+ * and the per-head A_log and dt_bias (bf16 [H]); beta = bf16(sigmoid(b)) and
+ * g = -exp(A_log) * softplus(a + dt_bias) are computed in the prep with cs1_gdn_gates'
+ * arithmetic, so each result equals cs1_gdn_gates followed by cs1_gdn_prefill_x (or _varlen)
+ * bit for bit, without the g / beta buffers or the extra launch.  Everything else (workspace,
+ * states, varlen rules, T = 0 pass-through) is that of the ungated form. */
+int cs1_gdn_prefill_gated_x(const void* q, const void* k, const void* v, const void* b, const void* a, int ld,
+                            const void* A_log, const void* dt_bias, void* o, float* workspace, int T, int H, int HK,
+                            float scale, const void* s_in, void* s_out, void* stream);
+int cs1_gdn_prefill_gated_varlen(const void* q, const void* k, const void* v, const void* b, const void* a, int ld,
+                                 const void* A_log, const void* dt_bias, void* o, float* workspace,
+                                 const int32_t* cu_seqlens, int nseq, int H, int HK, float scale, const void* s_in,
+                                 size_t s_in_stride, void* s_out, size_t s_out_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

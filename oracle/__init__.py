@@ -74,6 +74,8 @@ def lib():
                                     _nullable(np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")), c_int, f64p, nf64]
     L.orc_attention_emul.argtypes = [u16p, u16p, u16p, c_int, nu16, c_int, c_int, c_int, c_int, c_float, c_int,
                                      u16p, nf32]
+    L.orc_attention_emul_rows.argtypes = [u16p, u16p, u16p, c_int, nu16, c_int, c_int, c_int, c_int, c_float,
+                                          np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS"), c_int, u16p, nf32]
     L.orc_gdn_conv.argtypes = [u16p, c_int, u16p, u16p, u16p, u16p, c_int, c_int, c_int]
     L.orc_gdn_gates.argtypes = [u16p, u16p, c_int, u16p, u16p, u16p, f32p, c_int, c_int]
     L.orc_gated_rms_norm.argtypes = [u16p, u16p, c_int, u16p, u16p, c_int, c_int, c_int, c_float]
@@ -182,11 +184,17 @@ def attention_f64(q, k, v, ldv, T, Hq, Hk, Dh, scale, q_base=0, want_lse=False, 
     return (out, lse.reshape(Hq, T)) if want_lse else out
 
 
-def attention_emul(q, k, v, ldv, gate, T, Hq, Hk, Dh, scale, q_base=0, want_lse=False):
-    """Emulation of flash_kernel (attention.cu:84-234); out bf16 [T,Hq,Dh], lse f32 [Hq,T]."""
+def attention_emul(q, k, v, ldv, gate, T, Hq, Hk, Dh, scale, q_base=0, want_lse=False, rows=None):
+    """Emulation of flash_kernel (attention.cu:84-234); out bf16 [T,Hq,Dh], lse f32 [Hq,T].
+    ``rows`` restricts the work to those query rows (others stay zero; q_base is then unused)."""
     out = np.zeros(T * Hq * Dh, np.uint16)
     lse = np.zeros(Hq * T, np.float32) if want_lse else None
-    lib().orc_attention_emul(q, k, v, ldv, gate, T, Hq, Hk, Dh, scale, q_base, out, lse)
+    if rows is not None:
+        r = np.ascontiguousarray(rows, np.int32)
+        assert r.size == 0 or (r.min() >= 0 and r.max() < T)
+        lib().orc_attention_emul_rows(q, k, v, ldv, gate, T, Hq, Hk, Dh, scale, r, r.size, out, lse)
+    else:
+        lib().orc_attention_emul(q, k, v, ldv, gate, T, Hq, Hk, Dh, scale, q_base, out, lse)
     out = out.reshape(T, Hq, Dh)
     return (out, lse.reshape(Hq, T)) if want_lse else out
 

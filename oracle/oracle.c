@@ -421,57 +421,78 @@ void orc_attention_f64(const uint16_t* q, const uint16_t* k, const uint16_t* v, 
  * p; out = o / l, rounded to bf16, or with the gate
  * bf16(round_bf16(o / l) * round_bf16(sigmoid(gate))) (attention.cu:221-231).
  * lse (optional, [Hq, T]) = (m + log2 l) * ln 2, natural log. */
-void orc_attention_emul(const uint16_t* q, const uint16_t* k, const uint16_t* v, int ldv, const uint16_t* gate,
-                        int T, int Hq, int Hk, int Dh, float scale, int q_base, uint16_t* out, float* lse) {
+/* One query row i of orc_attention_emul (all heads): the row depends only on itself and the
+ * fixed key-tile order, so any subset of rows can be emulated on its own. */
+static void attention_emul_row(const uint16_t* q, const uint16_t* k, const uint16_t* v, int ldv, const uint16_t* gate,
+                               int T, int Hq, int Hk, int Dh, float scale, int i, float* o, uint16_t* out, float* lse) {
     const int group = Hq / Hk;
     const float sl2 = scale * 1.4426950408889634f;
+    float sc[32];
+    for (int h = 0; h < Hq; h++) {
+        const int gk = h / group;
+        const uint16_t* qi = q + ((size_t)i * Hq + h) * Dh;
+        float m = -INFINITY, l = 0.f;
+        for (int d = 0; d < Dh; d++) o[d] = 0.f;
+        for (int k0 = 0; k0 <= i; k0 += 32) {
+            float mx = -INFINITY;
+            for (int e = 0; e < 32; e++) {
+                const int key = k0 + e;
+                if (key <= i) {
+                    const uint16_t* kj = k + ((size_t)key * Hk + gk) * Dh;
+                    float acc = 0.f;
+                    for (int d = 0; d < Dh; d++) acc += bf(qi[d]) * bf(kj[d]);
+                    sc[e] = acc * sl2;
+                } else {
+                    sc[e] = -INFINITY;
+                }
+                mx = fmaxf(mx, sc[e]);
+            }
+            const float mn = fmaxf(m, mx);
+            const float base = mn == -INFINITY ? 0.f : mn;
+            const float alpha = exp2f(m - base);
+            m = mn;
+            l *= alpha;
+            for (int d = 0; d < Dh; d++) o[d] *= alpha;
+            for (int e = 0; e < 32; e++) {
+                const float p = exp2f(sc[e] - base);
+                l += p;
+                const float pr = rbf(p);
+                if (pr != 0.f) {
+                    const int key = k0 + e;
+                    for (int d = 0; d < Dh; d++) o[d] += pr * bf(v[(size_t)key * ldv + (size_t)gk * Dh + d]);
+                }
+            }
+        }
+        const float inv = 1.f / l;
+        for (int d = 0; d < Dh; d++) {
+            float a = o[d] * inv;
+            if (gate) a = rbf(a) * rbf(sigmoid_f(bf(gate[((size_t)i * Hq + h) * Dh + d])));
+            out[((size_t)i * Hq + h) * Dh + d] = f2bf(a);
+        }
+        if (lse) lse[(size_t)h * T + i] = (m + log2f(l)) * 0.6931471805599453f;
+    }
+}
+
+void orc_attention_emul(const uint16_t* q, const uint16_t* k, const uint16_t* v, int ldv, const uint16_t* gate,
+                        int T, int Hq, int Hk, int Dh, float scale, int q_base, uint16_t* out, float* lse) {
 #pragma omp parallel for schedule(dynamic)
     for (int i = q_base; i < T; i++) {
         float* o = (float*)malloc(sizeof(float) * Dh);
-        float sc[32];
-        for (int h = 0; h < Hq; h++) {
-            const int gk = h / group;
-            const uint16_t* qi = q + ((size_t)i * Hq + h) * Dh;
-            float m = -INFINITY, l = 0.f;
-            for (int d = 0; d < Dh; d++) o[d] = 0.f;
-            for (int k0 = 0; k0 <= i; k0 += 32) {
-                float mx = -INFINITY;
-                for (int e = 0; e < 32; e++) {
-                    const int key = k0 + e;
-                    if (key <= i) {
-                        const uint16_t* kj = k + ((size_t)key * Hk + gk) * Dh;
-                        float acc = 0.f;
-                        for (int d = 0; d < Dh; d++) acc += bf(qi[d]) * bf(kj[d]);
-                        sc[e] = acc * sl2;
-                    } else {
-                        sc[e] = -INFINITY;
-                    }
-                    mx = fmaxf(mx, sc[e]);
-                }
-                const float mn = fmaxf(m, mx);
-                const float base = mn == -INFINITY ? 0.f : mn;
-                const float alpha = exp2f(m - base);
-                m = mn;
-                l *= alpha;
-                for (int d = 0; d < Dh; d++) o[d] *= alpha;
-                for (int e = 0; e < 32; e++) {
-                    const float p = exp2f(sc[e] - base);
-                    l += p;
-                    const float pr = rbf(p);
-                    if (pr != 0.f) {
-                        const int key = k0 + e;
-                        for (int d = 0; d < Dh; d++) o[d] += pr * bf(v[(size_t)key * ldv + (size_t)gk * Dh + d]);
-                    }
-                }
-            }
-            const float inv = 1.f / l;
-            for (int d = 0; d < Dh; d++) {
-                float a = o[d] * inv;
-                if (gate) a = rbf(a) * rbf(sigmoid_f(bf(gate[((size_t)i * Hq + h) * Dh + d])));
-                out[((size_t)i * Hq + h) * Dh + d] = f2bf(a);
-            }
-            if (lse) lse[(size_t)h * T + i] = (m + log2f(l)) * 0.6931471805599453f;
-        }
+        attention_emul_row(q, k, v, ldv, gate, T, Hq, Hk, Dh, scale, i, o, out, lse);
+        free(o);
+    }
+}
+
+/* The same emulation restricted to the listed query rows (each in [0, T)); other rows of out
+ * and lse are left as they are. Long sequences are checked on sampled rows this way, as the
+ * reference's own test does for its float64 reference (kernels.rs:436-469). */
+void orc_attention_emul_rows(const uint16_t* q, const uint16_t* k, const uint16_t* v, int ldv, const uint16_t* gate,
+                             int T, int Hq, int Hk, int Dh, float scale, const int* rows, int nrows, uint16_t* out,
+                             float* lse) {
+#pragma omp parallel for schedule(dynamic)
+    for (int r = 0; r < nrows; r++) {
+        float* o = (float*)malloc(sizeof(float) * Dh);
+        attention_emul_row(q, k, v, ldv, gate, T, Hq, Hk, Dh, scale, rows[r], o, out, lse);
         free(o);
     }
 }

@@ -55,6 +55,15 @@ __device__ __forceinline__ float conv_silu(float x) {
     return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
 
+// GDN gates: beta = bf16(sigmoid(b)); g = -exp(A_log) * softplus(a + dt_bias), softplus(x) = x
+// above 20 (reference elementwise.cu:50-54; float32, expf/log1pf as PyTorch evaluates them).
+// Shared by cs1_gdn_gates and the gated GDN prefill, so the two give the same bits.
+__device__ __forceinline__ void gate_values(float b, float a, float neg_a_exp, float dt, bf16& beta, float& g) {
+    beta = to_bf16(sigmoid(b));
+    const float x = a + dt;
+    g = neg_a_exp * (x > 20.f ? x : log1pf(expf(x)));
+}
+
 // Butterfly sum over `width` consecutive lanes of a wave64 (width a power of two <= 64).
 template <int width>
 __device__ __forceinline__ float lane_sum(float x) {

@@ -201,14 +201,6 @@ __global__ void __launch_bounds__(THREADS)
 
 // ---- gates ----
 
-// beta = bf16(sigmoid(b)); g = -exp(A_log) * softplus(a + dt_bias), softplus(x) = x above 20
-// (reference elementwise.cu:50-54; float32, expf/log1pf as PyTorch evaluates them).
-__device__ __forceinline__ void gate_values(float b, float a, float neg_a_exp, float dt, bf16& beta, float& g) {
-    beta = to_bf16(sigmoid(b));
-    const float x = a + dt;
-    g = neg_a_exp * (x > 20.f ? x : log1pf(expf(x)));
-}
-
 // Rows of H heads with H % 8 == 0 and 16-byte aligned operands: a thread takes 8 heads of
 // one token (one 16-byte load of b and of a, one 16-byte beta store, two of g). The head
 // constants are loaded once per thread; threads of a block walk tokens with a grid stride.

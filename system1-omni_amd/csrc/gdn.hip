@@ -103,6 +103,32 @@ struct GSeqs {
     int tok[GSEQS_MAX + 1], chk[GSEQS_MAX + 1];
 };
 
+// The per-token gates of a launch: either precomputed (g float32, beta bf16, [T, H]) or, for
+// the gated entry points, the raw projections b and a (bf16 rows of stride ld, head h at
+// column h) with the per-head A_log and dt_bias, from which the prep computes beta and g with
+// the arithmetic of cs1_gdn_gates (gate_values), so both routes give the same bits.
+struct Gates {
+    const float* g;
+    const bf16* beta;
+    const bf16* b;
+    const bf16* a;
+    int ld;
+    const bf16* A_log;
+    const bf16* dt_bias;
+    // the gates of token rows from r0 on
+    __host__ __device__ Gates from_row(size_t r0, int H) const {
+        Gates x = *this;
+        if (b) {
+            x.b += r0 * ld;
+            x.a += r0 * ld;
+        } else {
+            x.g += r0 * H;
+            x.beta += r0 * H;
+        }
+        return x;
+    }
+};
+
 Work split(float* workspace, size_t NC, int H) {
     const Layout l(NC, H);
     unsigned char* b = reinterpret_cast<unsigned char*>(workspace);
@@ -303,10 +329,10 @@ __device__ __forceinline__ u32x4 staged_perm(const unsigned char* stg, int rl, i
     return u32x4{a[0], a[1], b[0], b[1]};
 }
 
+template <bool GATED>
 __global__ void __launch_bounds__(PT)
-    gdn_prep(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-             const float* __restrict__ g, const bf16* __restrict__ beta, Work ws, int T, int H, int HK, float scale,
-             const GSeqs gs) {
+    gdn_prep(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, Gates gt, Work ws,
+             int T, int H, int HK, float scale, const GSeqs gs) {
     extern __shared__ __align__(16) unsigned char sm[];
     u32x4* khi_pl = reinterpret_cast<u32x4*>(sm + R0);
     u32x4* klo_pl = reinterpret_cast<u32x4*>(sm + R0 + PLANE);
@@ -331,8 +357,7 @@ __global__ void __launch_bounds__(PT)
         q += (size_t)r0 * HK * DK;
         k += (size_t)r0 * HK * DK;
         v += (size_t)r0 * H * DK;
-        g += (size_t)r0 * H;
-        beta += (size_t)r0 * H;
+        gt = gt.from_row(r0, H);
     }
     const int hk = h / (H / HK);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
@@ -356,11 +381,18 @@ __global__ void __launch_bounds__(PT)
     //    transfers) and computes the decay for the block.
     const int tl = t0 + lane;
     float g_raw = 0.f;
-    uint32_t b_bits = 0;
+    uint32_t b_bits = 0, a_bits = 0, al_bits = 0, dt_bits = 0;
     if (wave == 0) {
         const int tlc = min(tl, T - 1);
-        asm volatile("global_load_dword %0, %1, off" : "=v"(g_raw) : "v"(g + (size_t)tlc * H + h));
-        asm volatile("global_load_ushort %0, %1, off" : "=v"(b_bits) : "v"(beta + (size_t)tlc * H + h));
+        if constexpr (GATED) {
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(b_bits) : "v"(gt.b + (size_t)tlc * gt.ld + h));
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(a_bits) : "v"(gt.a + (size_t)tlc * gt.ld + h));
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(al_bits) : "v"(gt.A_log + h));
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(dt_bits) : "v"(gt.dt_bias + h));
+        } else {
+            asm volatile("global_load_dword %0, %1, off" : "=v"(g_raw) : "v"(gt.g + (size_t)tlc * H + h));
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(b_bits) : "v"(gt.beta + (size_t)tlc * H + h));
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     const int qb = 3 - wave;
@@ -378,9 +410,19 @@ __global__ void __launch_bounds__(PT)
     // 1. cumulative log-decay, in index order (wave 0, lane = token), published through LDS
     //    at the barrier below
     if (wave == 0) {
-        asm volatile("s_waitcnt vmcnt(12)" : "+v"(g_raw), "+v"(b_bits));  // the 12 row transfers may be in flight
-        const float gv = tl < T ? g_raw : 0.f;
-        const float bv = tl < T ? __uint_as_float(b_bits << 16) : 0.f;
+        float gv, bv;
+        if constexpr (GATED) {
+            asm volatile("s_waitcnt vmcnt(12)" : "+v"(b_bits), "+v"(a_bits), "+v"(al_bits), "+v"(dt_bits));  // the 12 row transfers may be in flight
+            bf16 be;
+            float gg;
+            gate_values(f32((bf16)b_bits), f32((bf16)a_bits), -expf(f32((bf16)al_bits)), f32((bf16)dt_bits), be, gg);
+            gv = tl < T ? gg : 0.f;
+            bv = tl < T ? f32(be) : 0.f;
+        } else {
+            asm volatile("s_waitcnt vmcnt(12)" : "+v"(g_raw), "+v"(b_bits));
+            gv = tl < T ? g_raw : 0.f;
+            bv = tl < T ? __uint_as_float(b_bits << 16) : 0.f;
+        }
         float cs = 0.f;
         for (int j = 0; j < C; j++) {
             const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), j));
@@ -759,10 +801,10 @@ __device__ __forceinline__ void diag_inverse_preloaded(const float* am, float* t
     }
 }
 
+template <bool GATED>
 __global__ void __launch_bounds__(PT8)
-    gdn_prep8(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-              const float* __restrict__ g, const bf16* __restrict__ beta, Work ws, int T, int H, int HK, float scale,
-              const GSeqs gs) {
+    gdn_prep8(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v, Gates gt, Work ws,
+              int T, int H, int HK, float scale, const GSeqs gs) {
     extern __shared__ __align__(16) unsigned char sm[];
     u32x4* khi_pl = reinterpret_cast<u32x4*>(sm + R0);
     u32x4* klo_pl = reinterpret_cast<u32x4*>(sm + R0 + PLANE);
@@ -788,8 +830,7 @@ __global__ void __launch_bounds__(PT8)
         q += (size_t)r0 * HK * DK;
         k += (size_t)r0 * HK * DK;
         v += (size_t)r0 * H * DK;
-        g += (size_t)r0 * H;
-        beta += (size_t)r0 * H;
+        gt = gt.from_row(r0, H);
     }
     const int hk = h / (H / HK);
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, grp = lane >> 4;
@@ -815,11 +856,18 @@ __global__ void __launch_bounds__(PT8)
     // transfers issued after them: as ordinary loads the compiler placed the wait for beta, or
     // the loads themselves, after the transfers were issued or before them)
     float g_raw = 0.f;
-    uint32_t b_bits = 0;
+    uint32_t b_bits = 0, a_bits = 0, al_bits = 0, dt_bits = 0;
     if (wave == 3) {
         const int tlc = min(tl, T - 1);
-        asm volatile("global_load_dword %0, %1, off" : "=v"(g_raw) : "v"(g + (size_t)tlc * H + h));
-        asm volatile("global_load_ushort %0, %1, off" : "=v"(b_bits) : "v"(beta + (size_t)tlc * H + h));
+        if constexpr (GATED) {
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(b_bits) : "v"(gt.b + (size_t)tlc * gt.ld + h));
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(a_bits) : "v"(gt.a + (size_t)tlc * gt.ld + h));
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(al_bits) : "v"(gt.A_log + h));
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(dt_bits) : "v"(gt.dt_bias + h));
+        } else {
+            asm volatile("global_load_dword %0, %1, off" : "=v"(g_raw) : "v"(gt.g + (size_t)tlc * H + h));
+            asm volatile("global_load_ushort %0, %1, off" : "=v"(b_bits) : "v"(gt.beta + (size_t)tlc * H + h));
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     unsigned char* const stg = sm + (kside ? STG_K : STG_Q);
@@ -834,9 +882,19 @@ __global__ void __launch_bounds__(PT8)
     //    after term j (the same additions in the same order as a per-lane prefix loop)
     Q35_WSTAMP(0);
     if (wave == 3) {
-        asm volatile("s_waitcnt vmcnt(4)" : "+v"(g_raw), "+v"(b_bits));
-        const float gv = tl < T ? g_raw : 0.f;
-        const float bv = tl < T ? __uint_as_float(b_bits << 16) : 0.f;
+        float gv, bv;
+        if constexpr (GATED) {
+            asm volatile("s_waitcnt vmcnt(4)" : "+v"(b_bits), "+v"(a_bits), "+v"(al_bits), "+v"(dt_bits));
+            bf16 be;
+            float gg;
+            gate_values(f32((bf16)b_bits), f32((bf16)a_bits), -expf(f32((bf16)al_bits)), f32((bf16)dt_bits), be, gg);
+            gv = tl < T ? gg : 0.f;
+            bv = tl < T ? f32(be) : 0.f;
+        } else {
+            asm volatile("s_waitcnt vmcnt(4)" : "+v"(g_raw), "+v"(b_bits));
+            gv = tl < T ? g_raw : 0.f;
+            bv = tl < T ? __uint_as_float(b_bits << 16) : 0.f;
+        }
         float run = 0.f, cs = 0.f;
 #pragma unroll
         for (int j = 0; j < C; j++) {
@@ -1556,24 +1614,25 @@ Plan plan_segments(int T, int H) {
     return p;
 }
 
+// Form choices a test can force (-1: chosen by the launch shape). They are process-wide and
+// set only through q35_gdn_force_forms, a test hook outside the op ABI; the op entry points
+// never read the environment.
+std::atomic<int> force_prep_wide{-1}, force_prep_split{-1}, force_scan_halves{-1}, force_scan_osets{-1};
+
 // gdn_prep8 when every item gets a CU of its own (the launch is latency-bound); gdn_prep (three
-// 4-wave blocks per CU) otherwise. Overridable for tests by Q35_PREP_WIDE (0 or 1).
+// 4-wave blocks per CU) otherwise.
 bool prep_wide(long items) {
-    if (const char* e = getenv("Q35_PREP_WIDE")) {
-        if (e[0] == '0') return false;
-        if (e[0] == '1') return true;
-    }
+    const int f = force_prep_wide.load(std::memory_order_relaxed);
+    if (f >= 0) return f != 0;
     const int cus = device_cus();
     return cus > 0 && items <= cus;
 }
 
 // gdn_prep8 as two blocks per item (the inverse path and the q side on CUs of their own) when
-// twice the items still fit the device. Overridable for tests by Q35_PREP_SPLIT (0 or 1).
+// twice the items still fit the device.
 bool prep_split(long items) {
-    if (const char* e = getenv("Q35_PREP_SPLIT")) {
-        if (e[0] == '0') return false;
-        if (e[0] == '1') return true;
-    }
+    const int f = force_prep_split.load(std::memory_order_relaxed);
+    if (f >= 0) return f != 0;
     const int cus = device_cus();
     return cus > 0 && 2 * items <= cus;
 }
@@ -1582,36 +1641,42 @@ bool prep_split(long items) {
 // blocks of NSUB halves run in ceil(units * 8 / NSUB / CUs) rounds. The two-half block's chunk
 // step is ~1.46x the one-half block's (measured alone on the device: 1.24 vs 0.85 us), so it
 // is chosen when it saves enough rounds (config 2's 32 heads: one round either way, one half;
-// 48 heads: two rounds against one, two halves). Overridable for tests by Q35_SCAN_HALVES.
+// 48 heads: two rounds against one, two halves).
 int scan_halves(int units) {
-    if (const char* e = getenv("Q35_SCAN_HALVES")) {
-        const int v = atoi(e);
-        if (v == 1 || v == 2) return v;
-    }
+    const int f = force_scan_halves.load(std::memory_order_relaxed);
+    if (f == 1 || f == 2) return f;
     const long cus = device_cus();
     if (cus <= 0) return 1;
     const long r1 = ((long)units * 8 + cus - 1) / cus, r2 = ((long)units * 4 + cus - 1) / cus;
     return 146 * r2 < 100 * r1 ? 2 : 1;
 }
 
-// Output-wave sets of the one-half scan block (gdn_scan's OS). Overridable for tests by
-// Q35_SCAN_OSETS (1 or 2); both give the same bits.
+// Output-wave sets of the one-half scan block (gdn_scan's OS); both give the same bits.
 int scan_output_sets() {
-    if (const char* e = getenv("Q35_SCAN_OSETS")) {
-        const int v = atoi(e);
-        if (v == 1 || v == 2) return v;
-    }
-    return 2;
+    const int f = force_scan_osets.load(std::memory_order_relaxed);
+    return f == 1 ? 1 : 2;
 }
 
 // One launch pair over packed sequences (gs.n > 0: T is the total row count and gs
 // describes the sequences, their chunk offsets filled here) or over one sequence (or one
 // segment of it) of T rows.
-int gdn_launch(const void* q, const void* k, const void* v, const float* g, const void* beta, void* o,
-               float* workspace, int T, int H, int HK, float scale, const void* s_in, size_t s_in_stride,
-               void* s_out, size_t s_out_stride, GSeqs gs, hipStream_t st) {
-    static const hipError_t configured = hipFuncSetAttribute(reinterpret_cast<const void*>(gdn_prep),
-                                                             hipFuncAttributeMaxDynamicSharedMemorySize, PREP_SMEM);
+// The prep kernel's dynamic LDS limit, set once per process for each of its forms.
+template <typename K>
+hipError_t allow_smem(K kernel, int bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               bytes);
+}
+
+int gdn_launch(const void* q, const void* k, const void* v, const Gates& gt, void* o, float* workspace, int T, int H,
+               int HK, float scale, const void* s_in, size_t s_in_stride, void* s_out, size_t s_out_stride, GSeqs gs,
+               hipStream_t st) {
+    static const hipError_t configured = [] {
+        hipError_t e = allow_smem(gdn_prep<false>, PREP_SMEM);
+        if (e == hipSuccess) e = allow_smem(gdn_prep<true>, PREP_SMEM);
+        if (e == hipSuccess) e = allow_smem(gdn_prep8<false>, PREP8_SMEM);
+        if (e == hipSuccess) e = allow_smem(gdn_prep8<true>, PREP8_SMEM);
+        return e;
+    }();
     if (configured != hipSuccess) return configured;
     int NC = (T + C - 1) / C, nseq = 1;
     if (gs.n > 0) {
@@ -1622,18 +1687,15 @@ int gdn_launch(const void* q, const void* k, const void* v, const float* g, cons
     }
     if (NC == 0) return hipSuccess;
     const Work ws = split(workspace, NC, H);
+    const bf16 *qb = static_cast<const bf16*>(q), *kb = static_cast<const bf16*>(k), *vb = static_cast<const bf16*>(v);
+    const bool gated = gt.b != nullptr;
     if (prep_wide((long)NC * H)) {
-        static const hipError_t configured8 = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(gdn_prep8), hipFuncAttributeMaxDynamicSharedMemorySize, PREP8_SMEM);
-        if (configured8 != hipSuccess) return configured8;
-        const int roles = prep_split((long)NC * H) ? 2 : 1;
-        gdn_prep8<<<dim3(NC, H, roles), PT8, PREP8_SMEM, st>>>(static_cast<const bf16*>(q),
-                                                               static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                                                               g, static_cast<const bf16*>(beta), ws, T, H, HK, scale, gs);
+        const dim3 grid(NC, H, prep_split((long)NC * H) ? 2 : 1);
+        if (gated) gdn_prep8<true><<<grid, PT8, PREP8_SMEM, st>>>(qb, kb, vb, gt, ws, T, H, HK, scale, gs);
+        else gdn_prep8<false><<<grid, PT8, PREP8_SMEM, st>>>(qb, kb, vb, gt, ws, T, H, HK, scale, gs);
     } else {
-        gdn_prep<<<dim3(NC, H), PT, PREP_SMEM, st>>>(static_cast<const bf16*>(q), static_cast<const bf16*>(k),
-                                                     static_cast<const bf16*>(v), g, static_cast<const bf16*>(beta), ws,
-                                                     T, H, HK, scale, gs);
+        if (gated) gdn_prep<true><<<dim3(NC, H), PT, PREP_SMEM, st>>>(qb, kb, vb, gt, ws, T, H, HK, scale, gs);
+        else gdn_prep<false><<<dim3(NC, H), PT, PREP_SMEM, st>>>(qb, kb, vb, gt, ws, T, H, HK, scale, gs);
     }
     const int halves = scan_halves(H * nseq);
     const int osets = halves == 1 ? scan_output_sets() : 1;
@@ -1644,7 +1706,7 @@ int gdn_launch(const void* q, const void* k, const void* v, const float* g, cons
     return hipGetLastError();
 }
 
-int gdn_run(const void* q, const void* k, const void* v, const float* g, const void* beta, void* o, float* workspace,
+int gdn_run(const void* q, const void* k, const void* v, const Gates& gt, void* o, float* workspace,
             int T, int H, int HK, float scale, const void* s_in, size_t s_in_stride, void* s_out,
             size_t s_out_stride, GSeqs gs, void* stream) {
     if (T < 0 || H <= 0 || HK <= 0 || H % HK != 0) return hipErrorInvalidValue;
@@ -1662,11 +1724,11 @@ int gdn_run(const void* q, const void* k, const void* v, const float* g, const v
           reinterpret_cast<uintptr_t>(workspace)) & 15) != 0)
         return hipErrorInvalidValue;
     if (gs.n > 0)
-        return gdn_launch(q, k, v, g, beta, o, workspace, T, H, HK, scale, s_in, s_in_stride, s_out, s_out_stride, gs,
+        return gdn_launch(q, k, v, gt, o, workspace, T, H, HK, scale, s_in, s_in_stride, s_out, s_out_stride, gs,
                           st);
     const Plan p = plan_segments(T, H);
     if (p.seg >= p.NC)
-        return gdn_launch(q, k, v, g, beta, o, workspace, T, H, HK, scale, s_in, 0, s_out, 0, gs, st);
+        return gdn_launch(q, k, v, gt, o, workspace, T, H, HK, scale, s_in, 0, s_out, 0, gs, st);
     float* states[2] = {reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) + p.states),
                         reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) + p.states) +
                             (size_t)H * DK * DK};
@@ -1677,8 +1739,7 @@ int gdn_run(const void* q, const void* k, const void* v, const float* g, const v
         float* out = last ? so : states[j & 1];
         const int rc = gdn_launch(static_cast<const bf16*>(q) + (size_t)t0 * HK * DK,
                                   static_cast<const bf16*>(k) + (size_t)t0 * HK * DK,
-                                  static_cast<const bf16*>(v) + (size_t)t0 * H * DK, g + (size_t)t0 * H,
-                                  static_cast<const bf16*>(beta) + (size_t)t0 * H,
+                                  static_cast<const bf16*>(v) + (size_t)t0 * H * DK, gt.from_row(t0, H),
                                   static_cast<bf16*>(o) + (size_t)t0 * H * DK, workspace, len, H, HK, scale, cur_in, 0,
                                   out, 0, gs, st);
         if (rc != 0) return rc;
@@ -1701,6 +1762,24 @@ extern "C" int q35_debug_wave_ticks(unsigned long long* out) {
 }
 #endif
 
+// Test hook (no reference counterpart, not part of the op ABI): forces the prep and scan forms
+// that the bit-identity tests compare. -1 restores the shape-based choice. Every form gives the
+// same bits, so the hook changes only which kernels run.
+extern "C" int q35_gdn_force_forms(int prep_wide_, int prep_split_, int scan_halves_, int scan_osets_) {
+    force_prep_wide.store(prep_wide_, std::memory_order_relaxed);
+    force_prep_split.store(prep_split_, std::memory_order_relaxed);
+    force_scan_halves.store(scan_halves_, std::memory_order_relaxed);
+    force_scan_osets.store(scan_osets_, std::memory_order_relaxed);
+    return 0;
+}
+
+namespace {
+// precomputed gates (the reference's entry points)
+Gates given(const float* g, const void* beta) {
+    return Gates{g, static_cast<const bf16*>(beta), nullptr, nullptr, 0, nullptr, nullptr};
+}
+}  // namespace
+
 extern "C" size_t cs1_gdn_workspace_floats(int T, int H) {
     if (T < 0 || H < 0) return 0;
     return (plan_segments(T, std::max(H, 1)).total + 3) / 4;
@@ -1708,13 +1787,15 @@ extern "C" size_t cs1_gdn_workspace_floats(int T, int H) {
 
 extern "C" int cs1_gdn_prefill(const void* q, const void* k, const void* v, const float* g, const void* beta, void* o,
                                float* workspace, int T, int H, int HK, float scale, void* stream) {
-    return gdn_run(q, k, v, g, beta, o, workspace, T, H, HK, scale, nullptr, 0, nullptr, 0, GSeqs{0, {}, {}}, stream);
+    return gdn_run(q, k, v, given(g, beta), o, workspace, T, H, HK, scale, nullptr, 0, nullptr, 0, GSeqs{0, {}, {}},
+                   stream);
 }
 
 extern "C" int cs1_gdn_prefill_x(const void* q, const void* k, const void* v, const float* g, const void* beta,
                                  void* o, float* workspace, int T, int H, int HK, float scale, const void* s_in,
                                  void* s_out, void* stream) {
-    return gdn_run(q, k, v, g, beta, o, workspace, T, H, HK, scale, s_in, 0, s_out, 0, GSeqs{0, {}, {}}, stream);
+    return gdn_run(q, k, v, given(g, beta), o, workspace, T, H, HK, scale, s_in, 0, s_out, 0, GSeqs{0, {}, {}},
+                   stream);
 }
 
 // ---- cs1_gdn_prefill_x_static: the same launch pair with a library-owned workspace ----
@@ -1760,14 +1841,14 @@ extern "C" int cs1_gdn_prefill_x_static(const void* q, const void* k, const void
     void* ws = nullptr;
     const hipError_t e = device_scratch(&ws);
     if (e != hipSuccess) return e;
-    return gdn_run(q, k, v, g, beta, o, static_cast<float*>(ws), T, H, HK, scale, s_in, 0, s_out, 0,
+    return gdn_run(q, k, v, given(g, beta), o, static_cast<float*>(ws), T, H, HK, scale, s_in, 0, s_out, 0,
                    GSeqs{0, {}, {}}, stream);
 }
 
-extern "C" int cs1_gdn_prefill_varlen(const void* q, const void* k, const void* v, const float* g, const void* beta,
-                                      void* o, float* workspace, const int32_t* cu_seqlens, int nseq, int H, int HK,
-                                      float scale, const void* s_in, size_t s_in_stride, void* s_out,
-                                      size_t s_out_stride, void* stream) {
+namespace {
+int varlen_run(const void* q, const void* k, const void* v, const Gates& gt, void* o, float* workspace,
+               const int32_t* cu_seqlens, int nseq, int H, int HK, float scale, const void* s_in, size_t s_in_stride,
+               void* s_out, size_t s_out_stride, void* stream) {
     if (nseq < 0 || nseq > GSEQS_MAX) return hipErrorInvalidValue;
     if (nseq == 0) return hipSuccess;
     if (!cu_seqlens || cu_seqlens[0] != 0) return hipErrorInvalidValue;
@@ -1777,6 +1858,48 @@ extern "C" int cs1_gdn_prefill_varlen(const void* q, const void* k, const void* 
         if (i > 0 && cu_seqlens[i] < cu_seqlens[i - 1]) return hipErrorInvalidValue;
         gs.tok[i] = cu_seqlens[i];
     }
-    return gdn_run(q, k, v, g, beta, o, workspace, cu_seqlens[nseq], H, HK, scale, s_in, s_in_stride, s_out,
-                   s_out_stride, gs, stream);
+    return gdn_run(q, k, v, gt, o, workspace, cu_seqlens[nseq], H, HK, scale, s_in, s_in_stride, s_out, s_out_stride,
+                   gs, stream);
+}
+
+// The raw gate projections of the gated entry points; null when the arguments are invalid.
+bool raw_gates(const void* b, const void* a, int ld, const void* A_log, const void* dt_bias, int H, Gates* out) {
+    if (!b || !a || !A_log || !dt_bias || ld < H) return false;
+    *out = Gates{nullptr,
+                 nullptr,
+                 static_cast<const bf16*>(b),
+                 static_cast<const bf16*>(a),
+                 ld,
+                 static_cast<const bf16*>(A_log),
+                 static_cast<const bf16*>(dt_bias)};
+    return true;
+}
+}  // namespace
+
+extern "C" int cs1_gdn_prefill_varlen(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                                      void* o, float* workspace, const int32_t* cu_seqlens, int nseq, int H, int HK,
+                                      float scale, const void* s_in, size_t s_in_stride, void* s_out,
+                                      size_t s_out_stride, void* stream) {
+    return varlen_run(q, k, v, given(g, beta), o, workspace, cu_seqlens, nseq, H, HK, scale, s_in, s_in_stride, s_out,
+                      s_out_stride, stream);
+}
+
+extern "C" int cs1_gdn_prefill_gated_x(const void* q, const void* k, const void* v, const void* b, const void* a,
+                                       int ld, const void* A_log, const void* dt_bias, void* o, float* workspace,
+                                       int T, int H, int HK, float scale, const void* s_in, void* s_out,
+                                       void* stream) {
+    Gates gt{};
+    if (T > 0 && !raw_gates(b, a, ld, A_log, dt_bias, H, &gt)) return hipErrorInvalidValue;
+    return gdn_run(q, k, v, gt, o, workspace, T, H, HK, scale, s_in, 0, s_out, 0, GSeqs{0, {}, {}}, stream);
+}
+
+extern "C" int cs1_gdn_prefill_gated_varlen(const void* q, const void* k, const void* v, const void* b,
+                                            const void* a, int ld, const void* A_log, const void* dt_bias, void* o,
+                                            float* workspace, const int32_t* cu_seqlens, int nseq, int H, int HK,
+                                            float scale, const void* s_in, size_t s_in_stride, void* s_out,
+                                            size_t s_out_stride, void* stream) {
+    Gates gt{};
+    if (nseq > 0 && !raw_gates(b, a, ld, A_log, dt_bias, H, &gt)) return hipErrorInvalidValue;
+    return varlen_run(q, k, v, gt, o, workspace, cu_seqlens, nseq, H, HK, scale, s_in, s_in_stride, s_out,
+                      s_out_stride, stream);
 }

@@ -153,6 +153,10 @@ int describe(int M, int N, int K, int ldy, Plan& p) {
 // summation order, and so the rounding, changes from run to run. hipBLASLt names the
 // global-split-U algorithm of a kernel in its name ("GSUASB": single buffer, atomic
 // accumulation); the multiple-buffer form reduces through the workspace in a fixed order.
+// The naming was checked against the hipBLASLt of ROCm 7.2.0 (this image's library); the
+// public API exposes no attribute for the split-K accumulation mode. If a later library
+// renames these kernels, the cross-process bitwise test of the config-3 decision
+// (test_cfg3_decision_is_bitwise_repeatable_across_processes) is the guard that notices.
 bool accumulates_atomically(Gemm& g, hipblasLtMatmulAlgo_t& algo) {
     const std::string name = hipblaslt_ext::getKernelNameFromAlgo(g.handle, algo);
     return name.find("GSUASB") != std::string::npos;
@@ -213,7 +217,9 @@ int plan_for(Gemm& g, int M, int N, int K, int ldy, Plan*& out) {
     return new_plan(g, M, N, K, ldy, out);
 }
 
-bool valid(const Gemm* g, int M, int N, int K, int ldy) { return g && M >= 0 && N > 0 && K > 0 && ldy >= N; }
+bool valid(const Gemm* g, const void* x, const void* w, const void* y, int M, int N, int K, int ldy) {
+    return g && M >= 0 && N > 0 && K > 0 && ldy >= N && (M == 0 || (x && w && y));
+}
 
 }  // namespace
 
@@ -245,7 +251,7 @@ void cs1_gemm_destroy(void* gemm) {
 
 int cs1_gemm(void* gemm, const void* x, const void* w, void* y, int M, int N, int K, int ldy, void* stream) {
     Gemm* g = static_cast<Gemm*>(gemm);
-    if (!valid(g, M, N, K, ldy)) return hipErrorInvalidValue;
+    if (!valid(g, x, w, y, M, N, K, ldy)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
     Plan* p = nullptr;
     const int rc = plan_for(*g, M, N, K, ldy, p);
@@ -259,7 +265,13 @@ int cs1_gemm(void* gemm, const void* x, const void* w, void* y, int M, int N, in
             p->settled = true;
             return 0;
         }
-        if (p->settled || p->fallback.empty()) return status(s);
+        // Only a launch refused for the kernel itself moves the plan on (the operands were
+        // validated above, so these statuses come from the algorithm or its workspace; the
+        // stream-K refusal seen for 1217 x 2176 x 5120 with 32 MiB is status 6). Anything else
+        // is returned with the plan untouched, so a plan depends only on the shape.
+        const bool kernel_refused = s == HIPBLAS_STATUS_NOT_SUPPORTED || s == HIPBLAS_STATUS_INVALID_VALUE ||
+                                    s == HIPBLAS_STATUS_INTERNAL_ERROR;
+        if (p->settled || p->fallback.empty() || !kernel_refused) return status(s);
         p->algo = p->fallback.front();
         p->fallback.erase(p->fallback.begin());
         log_plan(*g, *p, M, N, K, "next choice after a rejected launch");
@@ -268,7 +280,7 @@ int cs1_gemm(void* gemm, const void* x, const void* w, void* y, int M, int N, in
 
 int cs1_gemm_tune(void* gemm, const void* x, const void* w, void* y, int M, int N, int K, int ldy, void* stream) {
     Gemm* g = static_cast<Gemm*>(gemm);
-    if (!valid(g, M, N, K, ldy)) return hipErrorInvalidValue;
+    if (!valid(g, x, w, y, M, N, K, ldy)) return hipErrorInvalidValue;
     if (M == 0) return hipSuccess;
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;

@@ -84,25 +84,34 @@ int cs1_stream_create(void** stream) {
 
 int cs1_stream_destroy(void* stream) { return settle(hipStreamDestroy(static_cast<hipStream_t>(stream))); }
 
+// A host wait on a capturing stream: refused, and the capture is marked spoilt.
+int refuse_host_wait(hipStream_t s) {
+    if (std::find(spoilt.begin(), spoilt.end(), s) == spoilt.end()) spoilt.push_back(s);
+    return hipErrorStreamCaptureUnsupported;
+}
+
 int cs1_stream_sync(void* stream) {
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (capturing(s)) {
-        if (std::find(spoilt.begin(), spoilt.end(), s) == spoilt.end()) spoilt.push_back(s);
-        return hipErrorStreamCaptureUnsupported;
-    }
+    if (capturing(s)) return refuse_host_wait(s);
     return settle(hipStreamSynchronize(s));
 }
 
 // Host <-> device copies are synchronous: they return once the bytes have arrived, in
-// stream order (the executor reuses its host buffers right after the call).
+// stream order (the executor reuses its host buffers right after the call). Both are host
+// waits, so under capture they are refused like cs1_stream_sync (a recorded copy would read or
+// write a host buffer the caller has already reused by the time the graph replays).
 int cs1_upload(void* dst, const void* src, size_t bytes, void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (capturing(s)) return refuse_host_wait(s);
     if (bytes == 0) return hipSuccess;
-    return settle(hipMemcpyWithStream(dst, src, bytes, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream)));
+    return settle(hipMemcpyWithStream(dst, src, bytes, hipMemcpyHostToDevice, s));
 }
 
 int cs1_download(void* dst, const void* src, size_t bytes, void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (capturing(s)) return refuse_host_wait(s);
     if (bytes == 0) return hipSuccess;
-    return settle(hipMemcpyWithStream(dst, src, bytes, hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream)));
+    return settle(hipMemcpyWithStream(dst, src, bytes, hipMemcpyDeviceToHost, s));
 }
 
 // Device copies are queued (and captured like kernels).

@@ -3,8 +3,10 @@
 // The op sequence is the reference executor's (src/models/qwen3_5/native/src/model.rs):
 //   embed ids -> res; x = rms_norm(res, input_norm[0])                     (1075-1098, 1143-1156)
 //   per layer:
-//     Gated DeltaNet: gdn_in = x W_in^T; conv1d + SiLU -> q, k, v; gates (b, a) -> beta, g;
-//       o = gdn_prefill(q, k, v, g, beta); ln = gated_rms_norm(o, z); delta = ln W_out^T
+//     Gated DeltaNet: gdn_in = x W_in^T; conv1d + SiLU -> q, k, v;
+//       o = gdn_prefill(q, k, v, gates(b, a)) (the gates computed inside the prefill: one launch
+//       pair instead of the reference's separate gates kernel); ln = gated_rms_norm(o, z);
+//       delta = ln W_out^T
 //                                                                          (1159-1233)
 //     full attention: attn_in = x W_qkv^T; attn_prep (q/k norm, RoPE, gate split);
 //       ao = attention_gated(q, k, v in place, gate); delta = ao W_o^T     (1234-1285)
@@ -148,7 +150,7 @@ struct Widths {
 };
 
 struct Scratch {
-    size_t ids, res, x, delta, gdn_in, lq, lk, lv, lo, ln, beta, g, ws, attn_in, aq, agate, ak, ao, gate_up, act,
+    size_t ids, res, x, delta, gdn_in, lq, lk, lv, lo, ln, ws, attn_in, aq, agate, ak, ao, gate_up, act,
         cos, sin, ccos, csin, hs, tgt, logits, lp, total;
 };
 
@@ -280,19 +282,19 @@ int for_groups(const Cands* cd, F&& f) {
 }
 
 // Packed Gated DeltaNet over the candidates, every candidate starting from the same captured
-// state.
-int gdn_candidates(Model& m, const Cands* cd, const void* q, const void* k, const void* v, const void* s0,
-                   float scale) {
+// state; the gates (b, a: rows of ld) are computed inside the prefill.
+int gdn_candidates(Model& m, const Cands* cd, const void* q, const void* k, const void* v, const unsigned char* b,
+                   const unsigned char* a, int ld, const Layer& L, const void* s0, float scale) {
     const Q35ModelConfig& c = m.cfg;
-    const size_t kd = m.w.kd * BF16, vd = m.w.vd * BF16;
+    const size_t kd = m.w.kd * BF16, vd = m.w.vd * BF16, row = (size_t)ld * BF16;
     return for_groups(cd, [&](int r0, const std::vector<int32_t>& cu) {
-        return cs1_gdn_prefill_varlen(static_cast<const unsigned char*>(q) + r0 * kd,
-                                      static_cast<const unsigned char*>(k) + r0 * kd,
-                                      static_cast<const unsigned char*>(v) + r0 * vd,
-                                      reinterpret_cast<const float*>(sc(m, m.s.g)) + (size_t)r0 * c.lin_v_heads,
-                                      sc(m, m.s.beta) + (size_t)r0 * c.lin_v_heads * BF16, sc(m, m.s.lo) + r0 * vd,
-                                      reinterpret_cast<float*>(sc(m, m.s.ws)), cu.data(), (int)cu.size() - 1,
-                                      c.lin_v_heads, c.lin_k_heads, scale, s0, 0, nullptr, 0, m.stream);
+        return cs1_gdn_prefill_gated_varlen(static_cast<const unsigned char*>(q) + r0 * kd,
+                                            static_cast<const unsigned char*>(k) + r0 * kd,
+                                            static_cast<const unsigned char*>(v) + r0 * vd, b + r0 * row,
+                                            a + r0 * row, ld, at(m, L.a_log), at(m, L.dt_bias),
+                                            sc(m, m.s.lo) + r0 * vd, reinterpret_cast<float*>(sc(m, m.s.ws)),
+                                            cu.data(), (int)cu.size() - 1, c.lin_v_heads, c.lin_k_heads, scale, s0, 0,
+                                            nullptr, 0, m.stream);
     });
 }
 
@@ -319,8 +321,6 @@ int run(Model& m, int T, Mode mode, const Cands* cd) {
             unsigned char* z = base + w.conv * BF16;
             unsigned char* b = z + w.vd * BF16;
             unsigned char* a = b + hv * BF16;
-            TRY(cs1_gdn_gates(b, a, ld, at(m, L.a_log), at(m, L.dt_bias), sc(m, s.beta),
-                              reinterpret_cast<float*>(sc(m, s.g)), T, hv, st));
             if (mode == CANDIDATES) {
                 // every candidate's convolution sees the prefix's last three pre-conv rows as
                 // its history, then the delta rule runs from the prefix's final state, each in
@@ -332,15 +332,16 @@ int run(Model& m, int T, Mode mode, const Cands* cd) {
                                                sc(m, s.lv) + (size_t)r0 * w.vd * BF16, cu.data(), (int)cu.size() - 1,
                                                m.pre.mem + m.pre.tail[li], (int)w.kd, (int)w.vd, st);
                 }));
-                TRY(gdn_candidates(m, cd, sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), m.pre.mem + m.pre.state[li],
-                                   gdn_scale));
+                TRY(gdn_candidates(m, cd, sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), b, a, ld, L,
+                                   m.pre.mem + m.pre.state[li], gdn_scale));
             } else {
                 TRY(cs1_gdn_conv(base, ld, at(m, L.conv), sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), T, (int)w.kd,
                                  (int)w.vd, st));
-                TRY(cs1_gdn_prefill_x(sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), reinterpret_cast<const float*>(sc(m, s.g)),
-                                      sc(m, s.beta), sc(m, s.lo), reinterpret_cast<float*>(sc(m, s.ws)), T, hv,
-                                      c.lin_k_heads, gdn_scale, nullptr,
-                                      mode == CAPTURE ? m.pre.mem + m.pre.state[li] : nullptr, st));
+                // the gates are computed inside the prefill (no separate cs1_gdn_gates launch)
+                TRY(cs1_gdn_prefill_gated_x(sc(m, s.lq), sc(m, s.lk), sc(m, s.lv), b, a, ld, at(m, L.a_log),
+                                            at(m, L.dt_bias), sc(m, s.lo), reinterpret_cast<float*>(sc(m, s.ws)), T,
+                                            hv, c.lin_k_heads, gdn_scale, nullptr,
+                                            mode == CAPTURE ? m.pre.mem + m.pre.state[li] : nullptr, st));
                 if (mode == CAPTURE)  // the last three pre-conv rows (model.rs:1427-1434)
                     TRY(cs1_copy_dd(m.pre.mem + m.pre.tail[li], base + (size_t)(T - 3) * gw, 3 * gw, st));
             }
@@ -604,8 +605,6 @@ int q35m_create(const Q35ModelConfig* cfg, uint64_t seed, int max_tokens, void**
     s.lv = buf(T * w.vd * BF16);
     s.lo = buf(T * w.vd * BF16);
     s.ln = buf(T * w.vd * BF16);
-    s.beta = buf(T * c.lin_v_heads * BF16);
-    s.g = buf(T * c.lin_v_heads * 4);
     // (packed candidates restart chunks per sequence: up to 64 more chunks per launch)
     s.ws = buf(cs1_gdn_workspace_floats(max_tokens + 64 * 64, c.lin_v_heads) * 4);
     s.attn_in = buf(T * w.attn_in * BF16);

@@ -82,6 +82,14 @@ ADDITIONS = {
     "cs1_gdn_prefill_varlen": (_I, [P, P, P, P, P, P, P, P, _I, _I, _I, c_float, P, _SZ, P, _SZ, P]),
     "cs1_gemm_tune": (_I, [P, P, P, P, _I, _I, _I, _I, P]),
     "cs1_gdn_prefill_x_static": (_I, [P, P, P, P, P, P, _I, _I, _I, c_float, P, P, P]),
+    "cs1_gdn_prefill_gated_x": (_I, [P, P, P, P, P, _I, P, P, P, P, _I, _I, _I, c_float, P, P, P]),
+    "cs1_gdn_prefill_gated_varlen": (_I, [P, P, P, P, P, _I, P, P, P, P, P, _I, _I, _I, c_float, P, _SZ, P, _SZ,
+                                          P]),
+}
+# ... and one test hook outside the op ABI: forces the GDN prep / scan kernel forms that the
+# bit-identity tests compare (-1: the shape-based choice)
+TEST_HOOKS = {
+    "q35_gdn_force_forms": (_I, [_I, _I, _I, _I]),
 }
 
 HIP_ERROR_INVALID_VALUE = 1
@@ -102,7 +110,7 @@ class Api:
     def __init__(self, lib: ctypes.CDLL, path: str):
         self._lib = lib
         self.path = path
-        for name, (res, args) in {**SYMBOLS, **ADDITIONS}.items():
+        for name, (res, args) in {**SYMBOLS, **ADDITIONS, **TEST_HOOKS}.items():
             try:
                 fn = getattr(lib, name)
             except AttributeError as e:

@@ -145,6 +145,41 @@ def test_config1_dh128_gated_with_lse(T):
     assert worst < 1.6e-2
 
 
+def test_north_star_shape_t8192_sampled_rows():
+    """The north-star attention shape (T = 8192, 16/4 heads, Dh 128, gated, LSE): 1024 row
+    blocks run longest-first over several rounds of the device. Checked on sampled rows, as
+    the reference checks long sequences (kernels.rs:393-474): the ungated output against
+    float64 (relative bar 1.6e-2), the LSE against float64 (1e-3), and the gated output and LSE
+    against the emulated reference kernel (bf16 max-abs 2e-2 / mean-abs 2e-3, LSE 1e-3)."""
+    T, Hq, Hk, Dh = 8192, 16, 4, 128
+    scale = Dh ** -0.5
+    say(f"attention north-star shape T={T} {Hq}/{Hk} Dh={Dh}, sampled rows")
+    q, k, v, gate = cfg1_inputs(T, Hq, Hk, Dh, seed=21)
+    rng = np.random.default_rng(22)
+    # the first and last rows of several row blocks (longest and shortest work items), the
+    # block boundaries around the middle, and random rows
+    rows = {0, 1, 31, 32, 63, 64, 4095, 4096, 8127, 8128, 8190, T - 1}
+    rows |= set(int(x) for x in rng.choice(T, 52, replace=False))
+    rows = sorted(rows)
+    dq, dk, dv, dg = dev(q), dev(k), dev(v), dev(gate)
+    out, lse = attn(dq, dk, dv, Hk * Dh, dg, T, Hq, Hk, Dh, scale, lse=True)
+    plain = attn(dq, dk, dv, Hk * Dh, None, T, Hq, Hk, Dh, scale)
+    assert np.isfinite(O.bf16_to_f32(out)).all() and np.isfinite(lse).all()
+    want, wlse = O.attention_f64(q, k, v, Hk * Dh, T, Hq, Hk, Dh, scale, want_lse=True, rows=rows)
+    pf = O.bf16_to_f32(plain).astype(np.float64)
+    worst = max(np.abs(pf[i, h] - want[i, h]).max() / max(1e-3, np.abs(want[i, h]).max()) for i in rows
+                for h in range(Hq))
+    say(f"  {len(rows)} rows: ungated vs float64 relative {worst:.2e}, "
+        f"lse vs float64 {np.abs(lse[:, rows] - wlse[:, rows]).max():.2e}")
+    assert worst < 1.6e-2
+    np.testing.assert_allclose(lse[:, rows], wlse[:, rows], atol=1e-3, rtol=0)
+    emu, else_ = O.attention_emul(q, k, v, Hk * Dh, gate, T, Hq, Hk, Dh, scale, want_lse=True, rows=rows)
+    mx, mean = bf16_errors(out[rows], O.bf16_to_f32(emu[rows]))
+    say(f"  gated vs emulated reference kernel: max-abs {mx:.2e} mean-abs {mean:.2e}")
+    assert mx <= 2e-2 and mean <= 2e-3
+    np.testing.assert_allclose(lse[:, rows], else_[:, rows], atol=1e-3, rtol=0)
+
+
 @pytest.mark.parametrize("hq,hk", [(32, 4), (8, 1), (12, 3)])
 def test_dh128_head_ratios_vs_emulator(hq, hk):
     """GQA ratios beyond 4 q heads per kv head and odd kv-head counts on the Dh=128 path."""

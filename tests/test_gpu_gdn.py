@@ -140,7 +140,7 @@ def test_gdn_prefill_two_phase_matches_one_shot_bit_for_bit():
 
 @pytest.mark.parametrize("t,h,hk,varlen", [(1000, 48, 16, False), (3399, 48, 16, False), (300, 32, 16, False),
                                             (0, 48, 16, True)])
-def test_gdn_scan_block_forms_are_bit_identical(t, h, hk, varlen, monkeypatch):
+def test_gdn_scan_block_forms_are_bit_identical(t, h, hk, varlen, forms):
     """The scan runs one or two 16-column halves per block (chosen by how many rounds of
     blocks the device needs: two halves at 48 heads, one at 32). Both forms must give the same
     bits, for single sequences with an initial state and for packed sequences."""
@@ -150,7 +150,7 @@ def test_gdn_scan_block_forms_are_bit_identical(t, h, hk, varlen, monkeypatch):
         q, k, v, g, b, s0 = cfg0_inputs(t, h, hk, seed=5, s0_std=0.01)
         runs = []
         for halves in ("1", "2"):
-            monkeypatch.setenv("Q35_SCAN_HALVES", halves)
+            forms(scan_halves=int(halves))
             runs.append(run_gdn(q, k, v, g, b, t, h, hk, s_in=s0, want_state=True))
         np.testing.assert_array_equal(runs[0][0], runs[1][0])
         np.testing.assert_array_equal(runs[0][1], runs[1][1])
@@ -163,7 +163,7 @@ def test_gdn_scan_block_forms_are_bit_identical(t, h, hk, varlen, monkeypatch):
     dq, dk, dv, dg, db, si = dev(q), dev(k), dev(v), dev(g), dev(b), dev(s0)
     outs = []
     for halves in ("1", "2"):
-        monkeypatch.setenv("Q35_SCAN_HALVES", halves)
+        forms(scan_halves=int(halves))
         o = empty(T * h * D * 2)
         so = empty(len(lens) * h * D * D * 4)
         ws = empty(api.cs1_gdn_workspace_floats(T + 64 * len(lens), h) * 4)
@@ -178,7 +178,7 @@ def test_gdn_scan_block_forms_are_bit_identical(t, h, hk, varlen, monkeypatch):
 @pytest.mark.parametrize("t,h,hk,varlen", [(64, 8, 4, False), (65, 8, 4, False), (130, 6, 3, False),
                                             (192, 16, 16, False), (300, 32, 16, False), (450, 8, 2, False),
                                             (8229, 32, 16, False), (0, 16, 8, True)])
-def test_gdn_scan_output_sets_are_bit_identical(t, h, hk, varlen, monkeypatch):
+def test_gdn_scan_output_sets_are_bit_identical(t, h, hk, varlen, forms):
     """The one-half scan block runs its output with one set of four waves or with two sets
     taking alternate chunks (bf16(S) and v_new double-buffered, the o stores in the next
     chunk's barrier windows). Both must give the same output and final state: chunk counts
@@ -186,12 +186,12 @@ def test_gdn_scan_output_sets_are_bit_identical(t, h, hk, varlen, monkeypatch):
     sequences including empty and one-row ones."""
     api, st = hip.api(), stream()
     say(f"gdn scan output sets t={t} h={h} hk={hk} varlen={varlen}")
-    monkeypatch.setenv("Q35_SCAN_HALVES", "1")
+    forms(scan_halves=1)
     if not varlen:
         q, k, v, g, b, s0 = cfg0_inputs(t, h, hk, seed=9, s0_std=0.01)
         runs = []
         for osets in ("1", "2"):
-            monkeypatch.setenv("Q35_SCAN_OSETS", osets)
+            forms(scan_halves=1, scan_osets=int(osets))
             runs.append(run_gdn(q, k, v, g, b, t, h, hk, s_in=s0, want_state=True))
         np.testing.assert_array_equal(runs[0][0], runs[1][0])
         np.testing.assert_array_equal(runs[0][1], runs[1][1])
@@ -204,7 +204,7 @@ def test_gdn_scan_output_sets_are_bit_identical(t, h, hk, varlen, monkeypatch):
     dq, dk, dv, dg, db, si = dev(q), dev(k), dev(v), dev(g), dev(b), dev(s0)
     outs = []
     for osets in ("1", "2"):
-        monkeypatch.setenv("Q35_SCAN_OSETS", osets)
+        forms(scan_halves=1, scan_osets=int(osets))
         o = empty(T * h * D * 2)
         so = empty(len(lens) * h * D * D * 4)
         ws = empty(api.cs1_gdn_workspace_floats(T + 64 * len(lens), h) * 4)
@@ -217,7 +217,7 @@ def test_gdn_scan_output_sets_are_bit_identical(t, h, hk, varlen, monkeypatch):
 
 
 @pytest.mark.parametrize("t,h,hk", [(512, 16, 16), (130, 6, 3), (107, 48, 16), (64, 8, 4)])
-def test_gdn_prep_forms_are_bit_identical(t, h, hk, monkeypatch):
+def test_gdn_prep_forms_are_bit_identical(t, h, hk, forms):
     """Launches whose chunks all fit on the device at once run the 8-wave prep (gdn_prep8),
     as two blocks per chunk when twice as many fit, the others the 4-wave one; every form must
     write the same records. The workspace starts as NaN bytes each time, so a record one form
@@ -230,8 +230,7 @@ def test_gdn_prep_forms_are_bit_identical(t, h, hk, monkeypatch):
     nws = api.cs1_gdn_workspace_floats(t, h)
     runs = []
     for wide, split in (("0", "0"), ("1", "0"), ("1", "1")):
-        monkeypatch.setenv("Q35_PREP_WIDE", wide)
-        monkeypatch.setenv("Q35_PREP_SPLIT", split)
+        forms(prep_wide=int(wide), prep_split=int(split))
         ws = dev(np.full(nws, 0xFFFFFFFF, np.uint32))
         o, so = empty(t * h * D * 2), empty(h * D * D * 4)
         hip.check(api.cs1_gdn_prefill_x(*(x.at(0) for x in bufs), o.at(0), ws.at(0), t, h, hk, D ** -0.5, si.at(0),
@@ -353,3 +352,98 @@ def test_gdn_varlen_arguments():
                                       None, 0, st.handle) != 0
     assert api.cs1_gdn_prefill_varlen(None, None, None, None, None, None, None, None, 0, 8, 4, 1.0, None, 0, None, 0,
                                       st.handle) == 0
+
+
+def gate_projections(T, H, ld, seed):
+    """Model-like raw gate inputs: rows of ld bf16 holding b at columns [0, H) and a at
+    [H, 2H) (the reference's projection layout), A_log = log U(0, 16) and dt_bias ~ 1 + N(0, 0.1)
+    (transformers' init, TF:816-820), with a spread that reaches the softplus threshold (x > 20)."""
+    rng = np.random.default_rng(seed)
+    rows = O.f32_to_bf16((rng.standard_normal((T, ld)) * 2.0).astype(np.float32)).reshape(T, ld)
+    rows[::7, H] = O.f32_to_bf16(np.float32([25.0]))[0]  # a + dt_bias above 20 on some tokens
+    A_log = O.f32_to_bf16(np.log(rng.uniform(1e-3, 16.0, H)).astype(np.float32))
+    dt = O.f32_to_bf16((1.0 + rng.standard_normal(H) * 0.1).astype(np.float32))
+    return rows.reshape(-1), A_log, dt
+
+
+@pytest.mark.parametrize("t,h,hk,prep", [(2000, 16, 8, "4-wave"), (130, 6, 3, "8-wave"), (107, 48, 16, "8-wave"),
+                                         (64, 8, 4, "split"), (8229, 32, 16, "segmented")])
+def test_gated_prefill_equals_gates_then_prefill(t, h, hk, prep, forms):
+    """cs1_gdn_prefill_gated_x (beta and g computed inside the prep from the raw projections)
+    equals cs1_gdn_gates followed by cs1_gdn_prefill_x bit for bit, outputs and final state, on
+    every prep form (4-wave, 8-wave, split 8-wave, and a segmented long sequence)."""
+    api, st = hip.api(), stream()
+    say(f"gated gdn prefill t={t} h={h} hk={hk} prep={prep}")
+    if prep == "split":
+        forms(prep_wide=1, prep_split=1)
+    elif prep == "8-wave":
+        forms(prep_wide=1, prep_split=0)
+    q, k, v, _, _, s0 = cfg0_inputs(t, h, hk, seed=31, s0_std=0.01)
+    ld = 2 * h + 24
+    rows, A_log, dt = gate_projections(t, h, ld, seed=32)
+    drows, dA, ddt = dev(rows), dev(A_log), dev(dt)
+    beta, g = empty(t * h * 2), empty(t * h * 4)
+    hip.check(api.cs1_gdn_gates(drows.at(0), drows.at(2 * h), ld, dA.at(0), ddt.at(0), beta.at(0), g.at(0), t, h,
+                                st.handle), "gates")
+    dq, dk, dv, si = dev(q), dev(k), dev(v), dev(s0)
+    ws = empty(api.cs1_gdn_workspace_floats(t, h) * 4)
+    o1, o2 = empty(t * h * D * 2), empty(t * h * D * 2)
+    so1, so2 = empty(h * D * D * 4), empty(h * D * D * 4)
+    hip.check(api.cs1_gdn_prefill_x(dq.at(0), dk.at(0), dv.at(0), g.at(0), beta.at(0), o1.at(0), ws.at(0), t, h, hk,
+                                    D ** -0.5, si.at(0), so1.at(0), st.handle), "ungated")
+    hip.check(api.cs1_gdn_prefill_gated_x(dq.at(0), dk.at(0), dv.at(0), drows.at(0), drows.at(2 * h), ld, dA.at(0),
+                                          ddt.at(0), o2.at(0), ws.at(0), t, h, hk, D ** -0.5, si.at(0), so2.at(0),
+                                          st.handle), "gated")
+    a_o, b_o = get_bf16(o1, t * h * D), get_bf16(o2, t * h * D)
+    assert np.isfinite(O.bf16_to_f32(b_o)).all()
+    np.testing.assert_array_equal(b_o, a_o)
+    np.testing.assert_array_equal(get(so2, np.float32, h * D * D), get(so1, np.float32, h * D * D))
+
+
+def test_gated_varlen_equals_gates_then_varlen():
+    """cs1_gdn_prefill_gated_varlen equals cs1_gdn_gates + cs1_gdn_prefill_varlen bit for bit
+    over packed sequences (empty and partial-chunk ones) from a shared initial state; argument
+    errors for missing gate inputs or ld < H."""
+    api, st = hip.api(), stream()
+    H, HK = 8, 4
+    lens = [0, 1, 63, 64, 65, 200, 7]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    say(f"gated gdn varlen lens={lens}")
+    q, k, v, _, _, _ = cfg0_inputs(T, H, HK, seed=33)
+    s0 = (np.random.default_rng(34).standard_normal((H, D, D)) * 0.05).astype(np.float32)
+    ld = 40
+    rows, A_log, dt = gate_projections(T, H, ld, seed=35)
+    drows, dA, ddt = dev(rows), dev(A_log), dev(dt)
+    beta, g = empty(T * H * 2), empty(T * H * 4)
+    hip.check(api.cs1_gdn_gates(drows.at(0), drows.at(2 * H), ld, dA.at(0), ddt.at(0), beta.at(0), g.at(0), T, H,
+                                st.handle), "gates")
+    dq, dk, dv, si = dev(q), dev(k), dev(v), dev(s0)
+    nch = int(sum((x + 63) // 64 for x in lens))
+    ws = empty(api.cs1_gdn_workspace_floats(64 * nch, H) * 4)
+    n = len(lens)
+    outs = []
+    for gated in (False, True):
+        o, so = empty(T * H * D * 2), empty(n * H * D * D * 4)
+        if gated:
+            rc = api.cs1_gdn_prefill_gated_varlen(dq.at(0), dk.at(0), dv.at(0), drows.at(0), drows.at(2 * H), ld,
+                                                  dA.at(0), ddt.at(0), o.at(0), ws.at(0), cu.ctypes.data, n, H, HK,
+                                                  D ** -0.5, si.at(0), 0, so.at(0), H * D * D, st.handle)
+        else:
+            rc = api.cs1_gdn_prefill_varlen(dq.at(0), dk.at(0), dv.at(0), g.at(0), beta.at(0), o.at(0), ws.at(0),
+                                            cu.ctypes.data, n, H, HK, D ** -0.5, si.at(0), 0, so.at(0), H * D * D,
+                                            st.handle)
+        hip.check(rc, f"varlen gated={gated}")
+        outs.append((get_bf16(o, T * H * D), get(so, np.float32, n * H * D * D)))
+    np.testing.assert_array_equal(outs[1][0], outs[0][0])
+    np.testing.assert_array_equal(outs[1][1], outs[0][1])
+    # argument errors: missing gate inputs, ld < H
+    assert api.cs1_gdn_prefill_gated_x(dq.at(0), dk.at(0), dv.at(0), None, drows.at(0), ld, dA.at(0), ddt.at(0),
+                                       None, ws.at(0), 64, H, HK, 1.0, None, None,
+                                       st.handle) == hip.HIP_ERROR_INVALID_VALUE
+    assert api.cs1_gdn_prefill_gated_x(dq.at(0), dk.at(0), dv.at(0), drows.at(0), drows.at(0), H - 1, dA.at(0),
+                                       ddt.at(0), None, ws.at(0), 64, H, HK, 1.0, None, None,
+                                       st.handle) == hip.HIP_ERROR_INVALID_VALUE
+    assert api.cs1_gdn_prefill_gated_varlen(dq.at(0), dk.at(0), dv.at(0), drows.at(0), drows.at(0), ld, None,
+                                            ddt.at(0), None, ws.at(0), cu.ctypes.data, n, H, HK, 1.0, None, 0, None,
+                                            0, st.handle) == hip.HIP_ERROR_INVALID_VALUE

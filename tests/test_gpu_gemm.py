@@ -77,6 +77,8 @@ def test_gemm_edge_arguments(gemm):
     assert api.cs1_gemm(gemm, None, None, None, 0, 16, 16, 16, st.handle) == 0
     assert api.cs1_gemm(gemm, None, None, None, 4, 16, 16, 8, st.handle) == hip.HIP_ERROR_INVALID_VALUE
     assert api.cs1_gemm(None, None, None, None, 4, 16, 16, 16, st.handle) == hip.HIP_ERROR_INVALID_VALUE
+    # null operands of a valid shape are an argument error, and the shape's plan is unaffected
+    assert api.cs1_gemm(gemm, None, None, None, 4, 16, 16, 16, st.handle) == hip.HIP_ERROR_INVALID_VALUE
 
 
 def test_gemm_tuned_and_default_plans_agree():

@@ -74,19 +74,27 @@ def test_graph_capture_failures_recover():
         api.cs1_graph_destroy(rec)
         # a host wait inside capture is refused (900) and spoils the capture: ending it reports
         # 901 and yields no graph, whether or not the recording passes the 900 on
-        for propagate in (True, False):
+        # (uploads and downloads are host waits too: the caller reuses its host buffer right
+        # after the call, so a copy recorded into a graph would replay stale or freed memory)
+        host = np.zeros(8, np.int32)
+        waits = {
+            "sync": lambda: api.cs1_stream_sync(st.handle),
+            "upload": lambda: api.cs1_upload(ids.at(0), host.ctypes.data, 32, st.handle),
+            "download": lambda: api.cs1_download(host.ctypes.data, ids.at(0), 32, st.handle),
+        }
+        for kind, propagate in [(k, p) for k in waits for p in (True, False)]:
             seen = []
 
             def record():
                 rc = embed()
                 if rc:
                     return rc
-                code = api.cs1_stream_sync(st.handle)
+                code = waits[kind]()
                 seen.append(code)
                 return code if propagate else 0
 
             rc, rec = _capture(st, record)
-            say(f"  sync inside capture (propagate={propagate}): sync {seen}, capture {rc}")
+            say(f"  {kind} inside capture (propagate={propagate}): wait {seen}, capture {rc}")
             assert seen == [hip.HIP_ERROR_STREAM_CAPTURE_UNSUPPORTED]
             assert rec is None
             assert rc == (hip.HIP_ERROR_STREAM_CAPTURE_UNSUPPORTED if propagate

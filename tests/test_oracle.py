@@ -220,6 +220,14 @@ def test_attention_emulator_gate_and_window():
     np.testing.assert_array_equal(fused, O.sigmoid_gate(plain, gate))
     win = O.attention_emul(q, k, v, Hk * Dh, gate, T, Hq, Hk, Dh, 0.08, q_base=64).reshape(T, -1)
     np.testing.assert_array_equal(win[64:], fused.reshape(T, -1)[64:])
+    # the row-restricted emulation equals the full one on those rows, and leaves the rest zero
+    rows = [0, 5, 64, 149]
+    out, lse = O.attention_emul(q, k, v, Hk * Dh, gate, T, Hq, Hk, Dh, 0.08, want_lse=True, rows=rows)
+    full, flse = O.attention_emul(q, k, v, Hk * Dh, gate, T, Hq, Hk, Dh, 0.08, want_lse=True)
+    np.testing.assert_array_equal(out[rows], full[rows])
+    np.testing.assert_array_equal(lse[:, rows], flse[:, rows])
+    others = np.setdiff1d(np.arange(T), rows)
+    assert not out[others].any() and not lse[:, others].any()
 
 
 # --------------------------------------------------------------- elementwise

@@ -47,14 +47,18 @@ def run_both(T, H, HK, seed):
 
 
 def test_static_workspace_matches_caller_workspace_twice():
-    run_both(1792, 32, 16, seed=1)   # the largest T at H = 32 (910 records: the whole array)
+    run_both(4480, 13, 1, seed=1)    # exactly 910 records (70 chunks x 13 heads): the whole array
+    run_both(1792, 32, 16, seed=3)   # the largest T at H = 32 (28 x 32 = 896 records)
     run_both(130, 8, 4, seed=2)      # smaller, a partial last chunk, other heads
 
 
 def test_static_workspace_limits():
     api, st = hip.api(), stream()
     say("gdn prefill static workspace: limits")
-    # 1793 tokens at 32 heads need 29 * 32 = 928 records > 910: refused before any launch
+    # 1793 tokens at 32 heads need 29 * 32 = 928 records > 910, 4481 at 13 heads 71 * 13 = 923:
+    # refused before any launch
+    assert api.cs1_gdn_prefill_x_static(None, None, None, None, None, None, 4481, 13, 1, 0.1, None, None,
+                                        st.handle) == hip.HIP_ERROR_INVALID_VALUE
     assert api.cs1_gdn_prefill_x_static(None, None, None, None, None, None, 1793, 32, 16, 0.1, None, None,
                                         st.handle) == hip.HIP_ERROR_INVALID_VALUE
     assert api.cs1_gdn_prefill_x_static(None, None, None, None, None, None, -1, 32, 16, 0.1, None, None,
