@@ -115,10 +115,12 @@ def test_config2_gdn_at_full_size():
 
 def test_gdn_prefill_two_phase_matches_one_shot_bit_for_bit():
     """kernels.rs:1049-1054; the 8192- and 8229-token cases run in segments (records over 200
-    MiB), so they also check that segmentation is invisible in the result."""
+    MiB), so they also check that segmentation is invisible in the result; the 22045-token case
+    runs as four segments, so the two ping-pong segment states are each written twice."""
     api, st = hip.api(), stream()
     for t, h, hk, amp, decay in [(107, 4, 2, 1.0, 1.0), (936, 4, 2, 0.01, 1.0), (3399, 3, 1, 0.01, 1.0),
-                                 (65, 4, 2, 0.01, 1e-9), (8192, 32, 16, 1.0, 0.01), (8229, 32, 16, 1.0, 0.01)]:
+                                 (65, 4, 2, 0.01, 1e-9), (8192, 32, 16, 1.0, 0.01), (8229, 32, 16, 1.0, 0.01),
+                                 (22045, 32, 16, 1.0, 0.01)]:
         say(f"gdn two-phase t={t} h={h} hk={hk}")
         q, k, v, g, b = O.gdn_test_inputs(t, h, hk, decay, amp)
         full, s_full = run_gdn(q, k, v, g, b, t, h, hk, want_state=True)
