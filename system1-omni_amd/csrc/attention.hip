@@ -1330,6 +1330,7 @@ int attention_run(const void* q, const void* k, const void* v, int ldv, const vo
         return hipErrorInvalidValue;
     if (q_base < 0 || q_base % 64 || q_base > T) return hipErrorInvalidValue;
     if (T == q_base) return hipSuccess;
+    if (!all_set({q, k, v, out})) return hipErrorInvalidValue;
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || (gate && !aligned16(gate)))
         return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1353,6 +1354,7 @@ int attention_varlen_run(const void* q, const void* k, const void* v, int ldv, c
     if (!cu_seqlens || cu_seqlens[0] != 0) return hipErrorInvalidValue;
     for (int i = 0; i < nseq; i++)
         if (cu_seqlens[i + 1] < cu_seqlens[i]) return hipErrorInvalidValue;
+    if (cu_seqlens[nseq] > 0 && !all_set({q, k, v, out})) return hipErrorInvalidValue;
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || (gate && !aligned16(gate)))
         return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1406,6 +1408,7 @@ extern "C" int cs1_attn_prep(const void* qg, const void* kr, int ld, const void*
     if ((Dh != 128 && Dh != 256) || half < 0 || half % 8 != 0 || 2 * half > Dh) return hipErrorInvalidValue;
     const int rows = T * (Hq + Hk);
     if (rows == 0) return hipSuccess;
+    if (!all_set({qg, kr, qw, kw, cos, sin, q, gate, k})) return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     auto args = [&](auto kernel, int rpb) {
         kernel<<<cdiv((size_t)rows, rpb), 256, 0, st>>>(

@@ -6,10 +6,19 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <initializer_list>
 
 #include "qwen3_5_ops.h"
 
 namespace q35 {
+
+// Operand pointers of a call that launches work: each must be set (a null operand is an
+// argument error, not a GPU fault).
+inline bool all_set(std::initializer_list<const void*> ps) {
+    for (const void* p : ps)
+        if (p == nullptr) return false;
+    return true;
+}
 
 // bfloat16 values are carried as raw 16-bit patterns in memory.
 using bf16 = uint16_t;

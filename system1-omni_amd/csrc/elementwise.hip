@@ -307,7 +307,7 @@ using namespace q35;
 extern "C" int cs1_embed(const int32_t* ids, const void* table, void* out, int T, int D, void* stream) {
     if (D % 8 != 0 || D < 0 || T < 0) return hipErrorInvalidValue;
     if (T == 0 || D == 0) return hipSuccess;
-    if (!aligned16(table) || !aligned16(out)) return hipErrorInvalidValue;
+    if (!all_set({ids, table, out}) || !aligned16(table) || !aligned16(out)) return hipErrorInvalidValue;
     const size_t total = (size_t)T * (D / 8);
     const unsigned blocks = (unsigned)std::min<size_t>(cdiv(total, THREADS), 2048);
     embed_rows<<<blocks, THREADS, 0, static_cast<hipStream_t>(stream)>>>(ids, static_cast<const Pack8*>(table),
@@ -321,6 +321,7 @@ extern "C" int cs1_gdn_conv(const void* qkv, int ld, const void* w, void* q, voi
     const int channels = 2 * key_dim + value_dim;
     const size_t n = (size_t)T * channels;
     if (n == 0) return hipSuccess;
+    if (!all_set({qkv, w, q, k, v})) return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const bool vec = key_dim % 8 == 0 && value_dim % 8 == 0 && ld % 8 == 0 && aligned16(qkv) && aligned16(w) &&
                      aligned16(q) && aligned16(k) && aligned16(v);
@@ -354,7 +355,7 @@ extern "C" int cs1_gdn_conv_varlen(const void* qkv, int ld, const void* w, void*
     if (nseq < 0 || nseq > CONV_SEQS_MAX || key_dim < 0 || value_dim < 0 || ld < 2 * key_dim + value_dim)
         return hipErrorInvalidValue;
     if (nseq == 0) return hipSuccess;
-    if (!cu_seqlens || cu_seqlens[0] != 0) return hipErrorInvalidValue;
+    if (!cu_seqlens || cu_seqlens[0] != 0 || !all_set({qkv, w, q, k, v})) return hipErrorInvalidValue;
     if (key_dim % 8 != 0 || value_dim % 8 != 0 || ld % 8 != 0 || !aligned16(qkv) || !aligned16(w) || !aligned16(q) ||
         !aligned16(k) || !aligned16(v) || (hist && !aligned16(hist)))
         return hipErrorInvalidValue;
@@ -382,6 +383,7 @@ extern "C" int cs1_gdn_gates(const void* b, const void* a, int ld, const void* A
     if (T < 0 || H < 0 || ld < H) return hipErrorInvalidValue;
     const size_t n = (size_t)T * H;
     if (n == 0) return hipSuccess;
+    if (!all_set({b, a, A_log, dt_bias, beta, g})) return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const bf16 *pb = static_cast<const bf16*>(b), *pa = static_cast<const bf16*>(a);
     const bf16 *pl = static_cast<const bf16*>(A_log), *pd = static_cast<const bf16*>(dt_bias);
@@ -398,6 +400,7 @@ extern "C" int cs1_gdn_gates(const void* b, const void* a, int ld, const void* A
 
 extern "C" int cs1_sigmoid_gate(void* x, const void* gate, size_t n, void* stream) {
     if (n == 0) return hipSuccess;
+    if (!all_set({x, gate})) return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (n % 8 == 0 && aligned16(x) && aligned16(gate))
         sigmoid_gate_vec_kernel<<<cdiv(n / 8, THREADS), THREADS, 0, st>>>(static_cast<Pack8*>(x),
@@ -412,6 +415,7 @@ extern "C" int cs1_silu_mul(const void* gate_up, int ld, void* out, int T, int I
     if (T < 0 || I < 0 || ld < 2 * I) return hipErrorInvalidValue;
     const size_t n = (size_t)T * I;
     if (n == 0) return hipSuccess;
+    if (!all_set({gate_up, out})) return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (I % 8 == 0 && ld % 8 == 0 && aligned16(gate_up) && aligned16(out))
         silu_mul_vec_kernel<<<cdiv(n / 8, THREADS), THREADS, 0, st>>>(static_cast<const Pack8*>(gate_up), ld / 8,

@@ -1720,6 +1720,8 @@ int gdn_run(const void* q, const void* k, const void* v, const Gates& gt, void* 
                                                   n4);
         return hipGetLastError();
     }
+    if (T > 0 && (!all_set({q, k, v, o, workspace}) || (gt.b == nullptr && !all_set({gt.g, gt.beta}))))
+        return hipErrorInvalidValue;
     if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
           reinterpret_cast<uintptr_t>(workspace)) & 15) != 0)
         return hipErrorInvalidValue;

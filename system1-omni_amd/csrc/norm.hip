@@ -175,12 +175,14 @@ using namespace q35;
 
 extern "C" int cs1_rms_norm(const void* x, const void* w, void* out, int rows, int D, float eps, void* stream) {
     if (rows <= 0 || D <= 0) return hipSuccess;
+    if (!all_set({x, w, out})) return hipErrorInvalidValue;
     return launch_rms<false>(nullptr, nullptr, x, w, out, rows, D, eps, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int cs1_add_rms_norm(void* residual, const void* delta, const void* w, void* out, int rows, int D,
                                 float eps, void* stream) {
     if (rows <= 0 || D <= 0) return hipSuccess;
+    if (!all_set({residual, delta, w, out})) return hipErrorInvalidValue;
     return launch_rms<true>(residual, delta, nullptr, w, out, rows, D, eps, static_cast<hipStream_t>(stream));
 }
 
@@ -189,6 +191,7 @@ extern "C" int cs1_gated_rms_norm(const void* x, const void* z, int ldz, const v
     if (D != 128 || ldz < H * D) return hipErrorInvalidValue;
     const int rows = T * H;
     if (rows <= 0) return hipSuccess;
+    if (!all_set({x, z, w, out})) return hipErrorInvalidValue;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const unsigned blocks = cdiv((size_t)rows, NORM_THREADS / 16);
     if (ldz % 8 == 0 && aligned16(x) && aligned16(z) && aligned16(w) && aligned16(out))

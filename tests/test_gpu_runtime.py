@@ -123,6 +123,48 @@ def test_empty_copies_and_null_frees_succeed():
     assert b"hipBLASLt" in api.cs1_error_string(1007)
 
 
+def test_null_operands_are_argument_errors():
+    """A call that would launch work with a null operand returns hipErrorInvalidValue (1) and
+    launches nothing; the same calls with nothing to do still succeed."""
+    api, st = hip.api(), stream()
+    say("runtime: null operands")
+    buf = empty(1 << 20)
+    x = buf.at(0)
+    cu = np.array([0, 64], np.int32)
+    h = st.handle
+    calls = {
+        "embed": lambda: api.cs1_embed(None, None, None, 4, 64, h),
+        "rms_norm": lambda: api.cs1_rms_norm(None, None, None, 4, 64, 1e-6, h),
+        "add_rms_norm": lambda: api.cs1_add_rms_norm(None, None, None, None, 4, 64, 1e-6, h),
+        "gated_rms_norm": lambda: api.cs1_gated_rms_norm(None, None, 128, None, None, 4, 1, 128, 1e-6, h),
+        "gdn_conv": lambda: api.cs1_gdn_conv(None, 24, None, None, None, None, 4, 8, 8, h),
+        "gdn_conv_varlen": lambda: api.cs1_gdn_conv_varlen(None, 24, None, None, None, None, cu.ctypes.data, 1, None,
+                                                           8, 8, h),
+        "gdn_gates": lambda: api.cs1_gdn_gates(None, None, 8, None, None, None, None, 4, 8, h),
+        "sigmoid_gate": lambda: api.cs1_sigmoid_gate(None, None, 64, h),
+        "silu_mul": lambda: api.cs1_silu_mul(None, 16, None, 4, 8, h),
+        "attn_prep": lambda: api.cs1_attn_prep(None, None, 1536, None, None, None, None, None, None, None, 4, 4, 1, 256,
+                                               32, 1e-6, h),
+        "attention_ex": lambda: api.cs1_attention_ex(None, None, None, 128, None, None, None, 64, 4, 1, 128, 0.1, 0, h),
+        "attention_varlen": lambda: api.cs1_attention_varlen(None, None, None, 128, None, None, None, cu.ctypes.data, 1,
+                                                             4, 1, 128, 0.1, h),
+        "gdn_prefill_x": lambda: api.cs1_gdn_prefill_x(None, None, None, None, None, None, None, 64, 2, 1, 0.1, None,
+                                                       None, h),
+        # every operand but g set: still an argument error
+        "gdn_prefill_x g": lambda: api.cs1_gdn_prefill_x(x, x, x, None, x, x, x, 64, 2, 1, 0.1, None, None, h),
+        "gdn_prefill_gated_x": lambda: api.cs1_gdn_prefill_gated_x(x, x, x, x, x, 2, x, x, None, x, 64, 2, 1, 0.1,
+                                                                   None, None, h),
+    }
+    for name, call in calls.items():
+        say(f"  {name}")
+        assert call() == 1, name
+    st.sync()
+    # nothing to do: success, whatever the pointers
+    assert api.cs1_embed(None, None, None, 0, 64, h) == 0
+    assert api.cs1_gdn_gates(None, None, 8, None, None, None, None, 0, 8, h) == 0
+    assert api.cs1_attention_ex(None, None, None, 128, None, None, None, 0, 4, 1, 128, 0.1, 0, h) == 0
+
+
 TINY = QM.Config(layers=4, hidden=256, intermediate=512, vocab=1024, heads=4, kv_heads=1, lin_k_heads=2,
                  lin_v_heads=4, lm_head=1)
 
