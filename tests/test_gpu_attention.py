@@ -180,6 +180,34 @@ def test_north_star_shape_t8192_sampled_rows():
     np.testing.assert_allclose(lse[:, rows], else_[:, rows], atol=1e-3, rtol=0)
 
 
+def test_t32768_sampled_rows():
+    """A long single sequence (T = 32768, 16/4 heads, Dh 128, gated, LSE): 4096 row blocks, rows
+    of up to 1024 steps per key group, many lazy rescales. Same checks and bars as the
+    north-star shape, on sampled rows."""
+    T, Hq, Hk, Dh = 32768, 16, 4, 128
+    scale = Dh ** -0.5
+    say(f"attention T={T} {Hq}/{Hk} Dh={Dh}, sampled rows")
+    q, k, v, gate = cfg1_inputs(T, Hq, Hk, Dh, seed=25)
+    rng = np.random.default_rng(26)
+    rows = sorted({0, 31, 32, 16383, 16384, 32735, 32736, T - 1} | set(int(x) for x in rng.choice(T, 16, replace=False)))
+    dq, dk, dv, dg = dev(q), dev(k), dev(v), dev(gate)
+    out, lse = attn(dq, dk, dv, Hk * Dh, dg, T, Hq, Hk, Dh, scale, lse=True)
+    plain = attn(dq, dk, dv, Hk * Dh, None, T, Hq, Hk, Dh, scale)
+    want, wlse = O.attention_f64(q, k, v, Hk * Dh, T, Hq, Hk, Dh, scale, want_lse=True, rows=rows)
+    pf = O.bf16_to_f32(plain).astype(np.float64)
+    worst = max(np.abs(pf[i, h] - want[i, h]).max() / max(1e-3, np.abs(want[i, h]).max()) for i in rows
+                for h in range(Hq))
+    say(f"  {len(rows)} rows: ungated vs float64 relative {worst:.2e}, "
+        f"lse vs float64 {np.abs(lse[:, rows] - wlse[:, rows]).max():.2e}")
+    assert worst < 1.6e-2
+    np.testing.assert_allclose(lse[:, rows], wlse[:, rows], atol=1e-3, rtol=0)
+    emu, else_ = O.attention_emul(q, k, v, Hk * Dh, gate, T, Hq, Hk, Dh, scale, want_lse=True, rows=rows)
+    mx, mean = bf16_errors(out[rows], O.bf16_to_f32(emu[rows]))
+    say(f"  gated vs emulated reference kernel: max-abs {mx:.2e} mean-abs {mean:.2e}")
+    assert mx <= 2e-2 and mean <= 2e-3
+    np.testing.assert_allclose(lse[:, rows], else_[:, rows], atol=1e-3, rtol=0)
+
+
 def test_dh256_t8192_sampled_rows():
     """The config-3 attention shape (16/4 heads, Dh 256, gated, LSE) at T = 8192: 1024 blocks of
     flash256_kernel over several rounds of the device. Sampled rows against float64 (ungated,
