@@ -82,6 +82,12 @@ int q35m_forward(void* model, const int32_t* ids, int T, float* last_hidden);
 /* forward, then logits[i] = float64 dot(embedding row label_ids[i], last hidden). */
 int q35m_decide(void* model, const int32_t* ids, int T, const int32_t* label_ids, int n_labels, float* logits);
 
+/* The decision head's arithmetic alone (host only, no device work), replacing
+ * src/models/cua_s1/native/src/executor.rs:61-78 letter_logits: logits[i] = (float) of the
+ * float64 sum over j of (double) letters[i * H + j] * (double) last[j], for rows i < n only
+ * (later rows are never read); hipErrorInvalidValue if any of the n logits is not finite. */
+int q35m_letter_logits(const float* letters, const float* last, int H, int n, float* logits);
+
 /* Prefix branching (the reference executor's capture / continue pair, model.rs:952-1073 and
  * run_window 1352-1571, with the candidate scoring of src/models/lfm2/engine.py:128-146).
  *

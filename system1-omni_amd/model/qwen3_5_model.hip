@@ -690,6 +690,21 @@ int q35m_forward(void* model, const int32_t* ids, int T, float* last_hidden) {
     return forward(*static_cast<Model*>(model), ids, T, last_hidden);
 }
 
+// executor.rs:61-78 letter_logits: logit i = (float) sum_j (double) letters[i H + j] (double) last[j]
+// in index order, rows i < n only; every logit is computed before any is checked, and a
+// non-finite one fails the call.
+int q35m_letter_logits(const float* letters, const float* last, int H, int n, float* logits) {
+    if (!letters || !last || !logits || H <= 0 || n <= 0) return hipErrorInvalidValue;
+    for (int i = 0; i < n; i++) {
+        double acc = 0.0;
+        for (int j = 0; j < H; j++) acc += (double)letters[(size_t)i * H + j] * (double)last[j];
+        logits[i] = (float)acc;
+    }
+    for (int i = 0; i < n; i++)
+        if (!std::isfinite(logits[i])) return hipErrorInvalidValue;
+    return 0;
+}
+
 int q35m_decide(void* model, const int32_t* ids, int T, const int32_t* label_ids, int n_labels, float* logits) {
     if (!model || !label_ids || n_labels <= 0 || !logits) return hipErrorInvalidValue;
     Model& m = *static_cast<Model*>(model);
@@ -698,21 +713,18 @@ int q35m_decide(void* model, const int32_t* ids, int T, const int32_t* label_ids
     const int H = m.cfg.hidden;
     std::vector<float> last(H);
     TRY(forward(m, ids, T, last.data()));
+    // the label rows of the bf16 embedding, as float32 (exact)
     std::vector<uint16_t> row(H);
+    std::vector<float> letters((size_t)n_labels * H);
     for (int i = 0; i < n_labels; i++) {
         TRY(cs1_download(row.data(), static_cast<unsigned char*>(at(m, m.embed)) + (size_t)label_ids[i] * H * BF16,
                          (size_t)H * BF16, m.stream));
-        double acc = 0.0;
         for (int j = 0; j < H; j++) {
             const uint32_t u = (uint32_t)row[j] << 16;
-            float f;
-            std::memcpy(&f, &u, 4);
-            acc += (double)f * (double)last[j];
+            std::memcpy(&letters[(size_t)i * H + j], &u, 4);
         }
-        logits[i] = (float)acc;
-        if (!std::isfinite(logits[i])) return hipErrorInvalidValue;
     }
-    return 0;
+    return q35m_letter_logits(letters.data(), last.data(), H, n_labels, logits);
 }
 
 int q35m_capture(void* model, const int32_t* ids, int P) {

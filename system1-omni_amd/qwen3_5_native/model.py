@@ -21,7 +21,7 @@ ATTN_QKV, ATTN_Q_NORM, ATTN_K_NORM, ATTN_O = 10, 11, 12, 13
 MLP_GATE_UP, MLP_DOWN, LM_HEAD = 14, 15, 16
 
 SYMBOLS = ["q35m_create", "q35m_destroy", "q35m_set_graph", "q35m_set_gemm_tuning", "q35m_forward", "q35m_decide", "q35m_capture",
-           "q35m_score", "q35m_logprobs", "q35m_tensor", "q35m_stream"]
+           "q35m_score", "q35m_logprobs", "q35m_tensor", "q35m_stream", "q35m_letter_logits"]
 
 
 class _Config(ctypes.Structure):
@@ -85,6 +85,7 @@ def load(path: str = None) -> ctypes.CDLL:
     lib.q35m_set_gemm_tuning.argtypes = [vp, ctypes.c_int]
     lib.q35m_forward.argtypes = [vp, i32p, ctypes.c_int, f32p]
     lib.q35m_decide.argtypes = [vp, i32p, ctypes.c_int, i32p, ctypes.c_int, f32p]
+    lib.q35m_letter_logits.argtypes = [f32p, f32p, ctypes.c_int, ctypes.c_int, f32p]
     lib.q35m_capture.argtypes = [vp, i32p, ctypes.c_int]
     lib.q35m_score.argtypes = [vp, i32p, i32p, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
     lib.q35m_logprobs.argtypes = [vp, i32p, ctypes.c_int, f32p]
@@ -93,6 +94,20 @@ def load(path: str = None) -> ctypes.CDLL:
     lib.q35m_stream.restype = vp
     _LIB = lib
     return lib
+
+
+def letter_logits(letters: np.ndarray, last: np.ndarray, n: int) -> np.ndarray:
+    """The decision head alone (q35m_letter_logits; executor.rs:61-78): float32 logits of the
+    first n rows of `letters` [*, H] against `last` [H], float64 accumulation. Raises
+    hip.HipError if a logit is not finite."""
+    lib = load()
+    letters = np.ascontiguousarray(letters, np.float32).reshape(-1)
+    last = np.ascontiguousarray(last, np.float32)
+    out = np.zeros(n, np.float32)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    hip.check(lib.q35m_letter_logits(letters.ctypes.data_as(f32p), last.ctypes.data_as(f32p), last.size, n,
+                                     out.ctypes.data_as(f32p)), "q35m_letter_logits")
+    return out
 
 
 def _cfg(c: Config) -> _Config:
