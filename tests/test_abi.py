@@ -1,7 +1,8 @@
 """The drop-in boundary, checked without a GPU.
 
 * libqwen3_5_hip.so loads, reports ABI 6 and exports every symbol include/qwen3_5_ops.h
-  declares; the reference loader's table (cuda.rs:50-133) is a subset of the header.
+  declares; the reference loader's table (cuda.rs:50-133) is a subset of the header;
+  libqwen3_5_model.so exports every symbol include/qwen3_5_model.h declares.
 * Argument validation returns hipErrorInvalidValue before any device work, with the
   reference's rules (attention.cu:239-243, 266-268; gdn_prefill.cu:571; elementwise.cu:97,
   106, 117, 134; norm.cu:281), and empty work succeeds without a launch.
@@ -116,7 +117,10 @@ def test_model_library_exports_and_validates():
     from qwen3_5_native import model as QM
 
     lib = QM.load()
-    for name in QM.SYMBOLS:
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "qwen3_5_model.h")).read(), flags=re.S)
+    declared = set(re.findall(r"\b(q35m_\w+)\s*\(", text))
+    assert declared and set(QM.SYMBOLS) <= declared
+    for name in declared:
         assert hasattr(lib, name), name
     bad = QM._cfg(QM.Config(layers=2, hidden=512, intermediate=1024, vocab=100, heads=4, kv_heads=3))
     h = ctypes.c_void_p()
