@@ -1219,6 +1219,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t stream_rsrc(const void* base) 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
 
+// The o rows of chunk c for one head and column slice (base = o + h * 128 + first column): a
+// buffer over the chunk's rows below T, so a lane stores with its fixed in-chunk offset and a
+// row past T falls outside the buffer and is dropped by the hardware (no per-row test).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rows(bf16* base, int c, int T, int H) {
+    // every value is wave-uniform; readfirstlane keeps the descriptor in scalar registers
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(C, T - c * C)));
+    const uint64_t a = (uint64_t)(base + (size_t)c * C * H * DK);
+    const uint64_t au = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(au), (short)0, rows * H * DK * 2, 0x00020000);
+}
+
 __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
@@ -1436,13 +1448,13 @@ __global__ void __launch_bounds__(256 + 256 * OS)
         f32x4 acc[NSUB];
         int pend = -1;  // the own chunk whose o waits to be stored
         auto store_rows = [&](int r0) {
+            const auto ro = out_rows(o + (size_t)h * DK + v0, pend, T, H);
 #pragma unroll
             for (int hf = 0; hf < NSUB; hf++)
 #pragma unroll
-                for (int r = r0; r < r0 + 2; r++) {
-                    const int t = pend * C + 16 * rb + 4 * grp + r;
-                    if (t < T) o[((size_t)t * H + h) * DK + v0 + 16 * hf + col] = to_bf16(acc[hf][r]);
-                }
+                for (int r = r0; r < r0 + 2; r++)
+                    __builtin_amdgcn_raw_buffer_store_b16(to_bf16(acc[hf][r]), ro,
+                                                          ((16 * rb + 4 * grp + r) * H * DK + 16 * hf + col) * 2, 0, 0);
         };
         auto own = [&](const OutOps& cur, int c) {
             const bf16* sbt = sbt_[c & 1];
@@ -1537,15 +1549,15 @@ __global__ void __launch_bounds__(256 + 256 * OS)
                 vb[hf][1] = lds_perm(vnt + 16 * hf * VLD, VLD, col, 1, grp);
             }
             __builtin_amdgcn_sched_barrier(0);
+            const auto ro = out_rows(o + (size_t)h * DK + v0, c, T, H);
 #pragma unroll
             for (int hf = 0; hf < NSUB; hf++) {
                 acc[hf] = mfma16(cur.pb[0], vb[hf][0], acc[hf]);
                 if (rb >= 2) acc[hf] = mfma16(cur.pb[1], vb[hf][1], acc[hf]);
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int t = c * C + 16 * rb + 4 * grp + r;
-                    if (t < T) o[((size_t)t * H + h) * DK + v0 + 16 * hf + col] = to_bf16(acc[hf][r]);
-                }
+                for (int r = 0; r < 4; r++)
+                    __builtin_amdgcn_raw_buffer_store_b16(to_bf16(acc[hf][r]), ro,
+                                                          ((16 * rb + 4 * grp + r) * H * DK + 16 * hf + col) * 2, 0, 0);
             }
         };
         OutOps opa, opb, opc, opd;
